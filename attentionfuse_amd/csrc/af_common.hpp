@@ -1,0 +1,174 @@
+// Shared device helpers for the gfx950 attention kernels: element types,
+// the 32x32x16 MFMA wrappers, register layouts, RoPE on 8-element chunks and
+// wave-level reductions.  gfx950 (CDNA4) only: wave64, 160 KiB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace af {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------------------
+// Element types.  Data moves as raw 16-byte chunks (u32x4 = 8 elements); the
+// traits convert chunks to/from fp32 and run the matching MFMA.
+// ---------------------------------------------------------------------------
+struct F16 {
+  using T = _Float16;
+  using V8 = f16x8;
+  __device__ static inline float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  }
+  __device__ static inline float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+  __device__ static inline uint32_t pack(float a, float b) {
+    uint16_t x = __builtin_bit_cast(uint16_t, (_Float16)a);
+    uint16_t y = __builtin_bit_cast(uint16_t, (_Float16)b);
+    return (uint32_t)x | ((uint32_t)y << 16);
+  }
+  __device__ static inline uint16_t one(float a) {
+    return __builtin_bit_cast(uint16_t, (_Float16)a);
+  }
+  __device__ static inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(
+        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+struct BF16 {
+  using T = __bf16;
+  using V8 = bf16x8;
+  __device__ static inline float lo(uint32_t w) {
+    return __builtin_bit_cast(float, w << 16);
+  }
+  __device__ static inline float hi(uint32_t w) {
+    return __builtin_bit_cast(float, w & 0xffff0000u);
+  }
+  __device__ static inline uint32_t pack(float a, float b) {
+    uint16_t x = __builtin_bit_cast(uint16_t, (__bf16)a);
+    uint16_t y = __builtin_bit_cast(uint16_t, (__bf16)b);
+    return (uint32_t)x | ((uint32_t)y << 16);
+  }
+  __device__ static inline uint16_t one(float a) {
+    return __builtin_bit_cast(uint16_t, (__bf16)a);
+  }
+  __device__ static inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+        0);
+  }
+  __device__ static inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+        0);
+  }
+};
+
+// Unpack a 16-byte chunk into 8 floats / pack 8 floats into a chunk.
+template <class E>
+__device__ inline void unpack8(u32x4 c, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = E::lo(c[i]);
+    f[2 * i + 1] = E::hi(c[i]);
+  }
+}
+template <class E>
+__device__ inline u32x4 pack8(const float* f) {
+  u32x4 c;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = E::pack(f[2 * i], f[2 * i + 1]);
+  return c;
+}
+
+// ---------------------------------------------------------------------------
+// 32x32x16 MFMA register layouts (wave64, lane l, half h = l / 32).
+//   A operand (32 x 16): lane holds row l%32, k-slots 8h .. 8h+7.
+//   B operand (16 x 32): lane holds column l%32, k-slots 8h .. 8h+7.
+//   C/D (32 x 32, 16 fp32): register r holds row 8*(r/4) + 4h + (r%4),
+//                            column l%32.
+// A and B pair the same k-slot of the same lane half, so any consistent
+// assignment of k indices to (h, slot) gives the same product.
+//
+// Score tiles are computed transposed, S^T = K * Q^T, with A-row i reading
+// key row kperm(i) (bits 2 and 3 of i swapped).  Then accumulator register r
+// of lane half h holds key 16*(r/8) + 8h + (r%8): the eight registers
+// 8j..8j+7 of a half are eight consecutive keys, which is exactly the B
+// operand of the P*V MFMA over keys 16j..16j+15 -- P^T feeds the second MFMA
+// straight from registers.  The column (query) is l%32 in both.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int kperm(int i) {
+  return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
+}
+__device__ __forceinline__ int acc_key(int r, int h) {
+  return 16 * (r >> 3) + 8 * h + (r & 7);
+}
+__device__ __forceinline__ int acc_row(int r, int h) {
+  return 8 * (r >> 2) + 4 * h + (r & 3);
+}
+
+// Partner lane l ^ 32 (the other half of a 32-wide MFMA column).
+__device__ __forceinline__ float xor32(float x) {
+  return __shfl_xor(x, 32, 64);
+}
+
+// ---------------------------------------------------------------------------
+// RoPE, rotate-half convention (reference: attnfuse/rope_utils.py:57-73):
+//   out[d]       = x[d] cos[d]       - x[d+D/2] sin[d]
+//   out[d+D/2]   = x[d+D/2] cos[d+D/2] + x[d] sin[d+D/2]
+// computed in fp32 and rounded once to the element type (the reference
+// rounds the rotated tile to the input dtype before the dot product,
+// attnfuse/compiler/codegen.py:126-135).
+// ---------------------------------------------------------------------------
+template <class E>
+__device__ inline void rope_pair(u32x4& lo, u32x4& hi, u32x4 clo, u32x4 slo,
+                                 u32x4 chi, u32x4 shi) {
+  float xl[8], xh[8], cl[8], sl[8], ch[8], sh[8], ol[8], oh[8];
+  unpack8<E>(lo, xl);
+  unpack8<E>(hi, xh);
+  unpack8<E>(clo, cl);
+  unpack8<E>(slo, sl);
+  unpack8<E>(chi, ch);
+  unpack8<E>(shi, sh);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    ol[i] = xl[i] * cl[i] - xh[i] * sl[i];
+    oh[i] = xh[i] * ch[i] + xl[i] * sh[i];
+  }
+  lo = pack8<E>(ol);
+  hi = pack8<E>(oh);
+}
+
+// Inverse (transpose) rotation applied to a gradient g of the rotated vector:
+//   dx[d]     = g[d] cos[d] + g[d+D/2] sin[d+D/2]
+//   dx[d+D/2] = g[d+D/2] cos[d+D/2] - g[d] sin[d]
+__device__ inline void rope_grad_pair(float& glo, float& ghi, float clo,
+                                      float slo, float chi, float shi) {
+  float a = glo * clo + ghi * shi;
+  float b = ghi * chi - glo * slo;
+  glo = a;
+  ghi = b;
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void st16(void* p, u32x4 v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+
+}  // namespace af

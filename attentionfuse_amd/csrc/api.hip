@@ -1,0 +1,313 @@
+// C ABI of libattnfuse_hip.so: argument validation, specialisation-key ->
+// instantiation selection and launch.  Declarations and the contract are in
+// include/attnfuse_hip.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "attnfuse_hip.h"
+#include "bwd_launch.hpp"
+#include "launch.hpp"
+#include "launch_decode.hpp"
+
+namespace af {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+namespace {
+
+constexpr int kKeysPerStage = 64;
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// (B, H, N, D) tensor with unit D-stride, 16-byte aligned rows.
+int check_bhnd(const char* name, const void* ptr, const int64_t* st) {
+  if (ptr == nullptr) return fail(AF_ERR_BAD_ARG, "%s is NULL", name);
+  if (st[3] != 1) return fail(AF_ERR_BAD_ARG, "%s: head-dim stride must be 1 (got %lld)", name, (long long)st[3]);
+  if (!aligned16(ptr)) return fail(AF_ERR_BAD_ARG, "%s: base pointer must be 16-byte aligned", name);
+  for (int i = 0; i < 3; ++i)
+    if (st[i] % 8 != 0)
+      return fail(AF_ERR_BAD_ARG, "%s: stride[%d]=%lld is not a multiple of 8 elements", name, i, (long long)st[i]);
+  return AF_OK;
+}
+
+int check_key(const af_spec_key& k, bool allow_bs) {
+  if (k.dtype != AF_F16 && k.dtype != AF_BF16)
+    return fail(AF_ERR_UNSUPPORTED, "dtype %d: the gfx950 kernels take fp16 or bf16", k.dtype);
+  if (k.head_dim != 32 && k.head_dim != 64 && k.head_dim != 128)
+    return fail(AF_ERR_UNSUPPORTED, "head_dim %d: instantiated for 32, 64 and 128", k.head_dim);
+  if (k.mask < 0 || k.mask > 3 || (!allow_bs && k.mask == AF_MASK_BLOCK_SPARSE))
+    return fail(AF_ERR_UNSUPPORTED, "mask kind %d not valid here", k.mask);
+  if (k.bias < 0 || k.bias > 2) return fail(AF_ERR_UNSUPPORTED, "bias kind %d", k.bias);
+  if (k.norm < 0 || k.norm > 1) return fail(AF_ERR_UNSUPPORTED, "norm kind %d", k.norm);
+  if (k.rope != 0 && k.rope != 1) return fail(AF_ERR_UNSUPPORTED, "rope kind %d", k.rope);
+  return AF_OK;
+}
+
+int check_fwd_common(const af_fwd_args* a) {
+  if (a == nullptr) return fail(AF_ERR_BAD_ARG, "args is NULL");
+  int rc;
+  if ((rc = check_bhnd("q", a->q, a->q_stride))) return rc;
+  if ((rc = check_bhnd("k", a->k, a->k_stride))) return rc;
+  if ((rc = check_bhnd("v", a->v, a->v_stride))) return rc;
+  if ((rc = check_bhnd("o", a->o, a->o_stride))) return rc;
+  if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seqlen_q < 0 || a->seqlen_kv < 0)
+    return fail(AF_ERR_BAD_ARG, "bad sizes B=%d Hq=%d Hkv=%d Nq=%d Nkv=%d", a->batch, a->heads_q,
+                a->heads_kv, a->seqlen_q, a->seqlen_kv);
+  if (a->heads_q % a->heads_kv != 0)
+    return fail(AF_ERR_BAD_ARG, "query heads (%d) must be a multiple of key/value heads (%d)", a->heads_q,
+                a->heads_kv);
+  const af_spec_key& k = a->key;
+  if ((k.mask == AF_MASK_CAUSAL || k.mask == AF_MASK_SLIDING_WINDOW) && a->seqlen_q != a->seqlen_kv)
+    return fail(AF_ERR_BAD_ARG, "causal / sliding-window masks need seqlen_q == seqlen_kv (%d vs %d)",
+                a->seqlen_q, a->seqlen_kv);
+  if (k.mask == AF_MASK_SLIDING_WINDOW && a->window <= 0)
+    return fail(AF_ERR_BAD_ARG, "sliding window size must be positive");
+  if (k.rope) {
+    if (a->cos == nullptr || a->sin == nullptr) return fail(AF_ERR_BAD_ARG, "rope needs cos and sin tables");
+    if (a->rope_stride[1] != 1 || a->rope_stride[0] % 8 != 0 || !aligned16(a->cos) || !aligned16(a->sin))
+      return fail(AF_ERR_BAD_ARG, "rope tables need unit d-stride, 16-byte aligned rows");
+    if (a->rope_len < std::max(a->seqlen_q, a->seqlen_kv))
+      return fail(AF_ERR_BAD_ARG, "rope tables have %d rows, need %d", a->rope_len,
+                  std::max(a->seqlen_q, a->seqlen_kv));
+  }
+  if (k.bias == AF_BIAS_ALIBI && a->alibi_slopes == nullptr) return fail(AF_ERR_BAD_ARG, "ALiBi needs slopes");
+  if (k.bias == AF_BIAS_ADDITIVE) {
+    if (a->bias == nullptr) return fail(AF_ERR_BAD_ARG, "additive bias pointer is NULL");
+    if (a->bias_stride[3] != 1 || !aligned16(a->bias) || a->bias_stride[0] % 8 || a->bias_stride[1] % 8 ||
+        a->bias_stride[2] % 8)
+      return fail(AF_ERR_BAD_ARG, "additive bias needs unit key stride and 16-byte aligned rows");
+  }
+  return AF_OK;
+}
+
+FwdParams make_fwd_params(const af_fwd_args* a, int bm) {
+  FwdParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.o = static_cast<uint16_t*>(a->o);
+  p.lse = a->lse;
+  p.cos = static_cast<const uint16_t*>(a->cos);
+  p.sin = static_cast<const uint16_t*>(a->sin);
+  p.slopes = a->alibi_slopes;
+  p.bias = static_cast<const uint16_t*>(a->bias);
+  p.coverage = a->coverage;
+  for (int i = 0; i < 4; ++i) {
+    p.qs[i] = a->q_stride[i];
+    p.ks[i] = a->k_stride[i];
+    p.vs[i] = a->v_stride[i];
+    p.os[i] = a->o_stride[i];
+    p.bs[i] = a->bias_stride[i];
+  }
+  for (int i = 0; i < 3; ++i) p.ls[i] = a->lse_stride[i];
+  p.rs[0] = a->rope_stride[0];
+  p.rs[1] = a->rope_stride[1];
+  p.B = a->batch;
+  p.Hq = a->heads_q;
+  p.Hkv = a->heads_kv;
+  p.Nq = a->seqlen_q;
+  p.Nkv = a->seqlen_kv;
+  p.G = a->heads_q / a->heads_kv;
+  p.n_mblocks = (a->seqlen_q + bm - 1) / bm;
+  p.cov_nq = (a->seqlen_q + 31) / 32;
+  p.cov_nk = (a->seqlen_kv + kKeysPerStage - 1) / kKeysPerStage;
+  p.scale = a->scale;
+  p.window = a->window;
+  return p;
+}
+
+int dispatch_fwd(const FwdParams& p, const af_spec_key& k, int waves, hipStream_t s) {
+  const dim3 grid((unsigned)p.n_mblocks * (unsigned)(p.B * p.Hq));
+  int rc = -1;
+  const bool f16 = k.dtype == AF_F16;
+  switch (k.head_dim) {
+    case 32:
+      rc = f16 ? launch_fwd_f16_d32(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s)
+               : launch_fwd_bf16_d32(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s);
+      break;
+    case 64:
+      rc = f16 ? launch_fwd_f16_d64(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s)
+               : launch_fwd_bf16_d64(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s);
+      break;
+    case 128:
+      rc = f16 ? launch_fwd_f16_d128(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s)
+               : launch_fwd_bf16_d128(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s);
+      break;
+  }
+  if (rc != 0) return fail(AF_ERR_UNSUPPORTED, "no forward instantiation for this key");
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(AF_ERR_LAUNCH, "forward launch failed: %s", hipGetErrorString(e));
+  return AF_OK;
+}
+
+}  // namespace
+}  // namespace af
+
+using namespace af;
+
+extern "C" {
+
+const char* af_last_error(void) { return g_err; }
+
+int af_abi_version(void) { return AF_ABI_VERSION; }
+
+int af_query(const af_spec_key* key) {
+  if (key == nullptr) return 0;
+  return check_key(*key, true) == AF_OK ? 1 : 0;
+}
+
+int af_fwd_tile(const af_spec_key* key, int32_t* block_m, int32_t* block_n) {
+  if (key == nullptr) return fail(AF_ERR_BAD_ARG, "key is NULL");
+  int rc = check_key(*key, true);
+  if (rc) return rc;
+  if (block_m) *block_m = 128;
+  if (block_n) *block_n = kKeysPerStage;
+  return AF_OK;
+}
+
+int af_fwd(const af_fwd_args* a, void* stream) {
+  int rc = check_fwd_common(a);
+  if (rc) return rc;
+  if ((rc = check_key(a->key, false))) return rc;
+  if (a->seqlen_q == 0) return AF_OK;
+  const FwdParams p = make_fwd_params(a, 128);
+  return dispatch_fwd(p, a->key, 4, static_cast<hipStream_t>(stream));
+}
+
+int af_fwd_blocksparse(const af_fwd_args* a, const af_blockmask* bm, void* stream) {
+  int rc = check_fwd_common(a);
+  if (rc) return rc;
+  if ((rc = check_key(a->key, true))) return rc;
+  if (a->key.mask != AF_MASK_BLOCK_SPARSE)
+    return fail(AF_ERR_BAD_ARG, "af_fwd_blocksparse needs key.mask == AF_MASK_BLOCK_SPARSE");
+  if (bm == nullptr || bm->full_kv_num == nullptr || bm->full_kv_idx == nullptr ||
+      bm->kv_num_blocks == nullptr || bm->kv_indices == nullptr)
+    return fail(AF_ERR_BAD_ARG, "block mask lists are NULL");
+  if (bm->block_m != 32 && bm->block_m != 64 && bm->block_m != 128)
+    return fail(AF_ERR_UNSUPPORTED, "block-sparse BLOCK_M=%d: supported 32, 64, 128", bm->block_m);
+  if (bm->block_n <= 0 || bm->block_n % kKeysPerStage != 0)
+    return fail(AF_ERR_UNSUPPORTED, "block-sparse BLOCK_N=%d: must be a multiple of 64", bm->block_n);
+  if (bm->n_q_blocks != (a->seqlen_q + bm->block_m - 1) / bm->block_m ||
+      bm->n_kv_blocks != (a->seqlen_kv + bm->block_n - 1) / bm->block_n)
+    return fail(AF_ERR_BAD_ARG, "block mask grid %dx%d does not match sequence lengths %d/%d", bm->n_q_blocks,
+                bm->n_kv_blocks, a->seqlen_q, a->seqlen_kv);
+  if (a->seqlen_q == 0) return AF_OK;
+  FwdParams p = make_fwd_params(a, bm->block_m);
+  p.bs_full_num = bm->full_kv_num;
+  p.bs_full_idx = bm->full_kv_idx;
+  p.bs_part_num = bm->kv_num_blocks;
+  p.bs_part_idx = bm->kv_indices;
+  p.bs_full_rs = bm->full_kv_stride;
+  p.bs_part_rs = bm->kv_stride;
+  p.bs_block_n = bm->block_n;
+  return dispatch_fwd(p, a->key, bm->block_m / 32, static_cast<hipStream_t>(stream));
+}
+
+int32_t af_decode_num_splits(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seqlen_kv,
+                             int32_t head_dim) {
+  (void)head_dim;
+  if (batch <= 0 || heads_q <= 0 || heads_kv <= 0 || seqlen_kv <= 0) return 1;
+  const int g = heads_q / heads_kv;
+  const int64_t groups = (int64_t)batch * heads_kv * ((g + 15) / 16);
+  // ~1024 workgroups (4 per CU on 256 CUs), at least 256 keys per split.
+  int64_t s = (1024 + groups - 1) / groups;
+  s = std::min<int64_t>(s, std::max<int64_t>(1, seqlen_kv / 256));
+  s = std::max<int64_t>(1, std::min<int64_t>(s, 256));
+  return (int32_t)s;
+}
+
+size_t af_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t head_dim, int32_t num_splits) {
+  if (batch <= 0 || heads_q <= 0 || head_dim <= 0 || num_splits <= 0) return 0;
+  return (size_t)num_splits * batch * heads_q * (2 + head_dim) * sizeof(float);
+}
+
+int af_decode(const af_decode_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  if (a == nullptr) return fail(AF_ERR_BAD_ARG, "args is NULL");
+  int rc;
+  if ((rc = check_bhnd("q", a->q, a->q_stride))) return rc;
+  if ((rc = check_bhnd("k", a->k, a->k_stride))) return rc;
+  if ((rc = check_bhnd("v", a->v, a->v_stride))) return rc;
+  if (a->o == nullptr) return fail(AF_ERR_BAD_ARG, "o is NULL");
+  if (a->o_stride[3] != 1) return fail(AF_ERR_BAD_ARG, "o: head-dim stride must be 1");
+  if ((rc = check_key(a->key, false))) return rc;
+  if (a->key.mask != AF_MASK_FULL || a->key.rope != 0 || a->key.norm != AF_NORM_SOFTMAX ||
+      (a->key.bias != AF_BIAS_NONE && a->key.bias != AF_BIAS_ALIBI))
+    return fail(AF_ERR_UNSUPPORTED, "decode takes dense softmax with no bias or ALiBi, no RoPE");
+  if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seqlen_kv <= 0 ||
+      a->heads_q % a->heads_kv != 0)
+    return fail(AF_ERR_BAD_ARG, "bad decode sizes B=%d Hq=%d Hkv=%d Nkv=%d", a->batch, a->heads_q, a->heads_kv,
+                a->seqlen_kv);
+  if (a->key.bias == AF_BIAS_ALIBI && a->alibi_slopes == nullptr) return fail(AF_ERR_BAD_ARG, "ALiBi needs slopes");
+  const int D = a->key.head_dim;
+  int S = a->num_splits > 0 ? a->num_splits
+                            : af_decode_num_splits(a->batch, a->heads_q, a->heads_kv, a->seqlen_kv, D);
+  int split_len = (a->seqlen_kv + S - 1) / S;
+  split_len = (split_len + 31) & ~31;
+  S = (a->seqlen_kv + split_len - 1) / split_len;  // drop empty trailing splits
+  const size_t need = af_decode_workspace_bytes(a->batch, a->heads_q, D, S);
+  if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+    return fail(AF_ERR_WORKSPACE, "decode workspace needs %zu bytes (16-byte aligned), got %zu", need,
+                workspace_bytes);
+  DecodeParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.o = static_cast<uint16_t*>(a->o);
+  p.slopes = a->alibi_slopes;
+  const size_t rows = (size_t)S * a->batch * a->heads_q;
+  p.ws_ml = static_cast<float*>(workspace);
+  p.ws_acc = p.ws_ml + 2 * rows;
+  for (int i = 0; i < 4; ++i) {
+    p.qs[i] = a->q_stride[i];
+    p.ks[i] = a->k_stride[i];
+    p.vs[i] = a->v_stride[i];
+    p.os[i] = a->o_stride[i];
+  }
+  p.B = a->batch;
+  p.Hq = a->heads_q;
+  p.Hkv = a->heads_kv;
+  p.Nkv = a->seqlen_kv;
+  p.G = a->heads_q / a->heads_kv;
+  p.nqc = (p.G + 15) / 16;
+  p.nsplit = S;
+  p.split_len = split_len;
+  p.scale = a->scale;
+  const dim3 gs((unsigned)S, (unsigned)(a->batch * a->heads_kv * p.nqc));
+  const dim3 gc((unsigned)((a->batch * a->heads_q + 3) / 4));
+  if (launch_decode(p, a->key.dtype, D, a->key.bias, gs, gc, static_cast<hipStream_t>(stream)) != 0)
+    return fail(AF_ERR_UNSUPPORTED, "no decode instantiation for this key");
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(AF_ERR_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
+  return AF_OK;
+}
+
+size_t af_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q) {
+  return bwd_workspace_bytes(batch, heads_q, seqlen_q);
+}
+
+int af_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_t workspace_bytes,
+           void* stream) {
+  return run_bwd(a, bm, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,260 @@
+// Flash-decoding for gfx950 (piece (b)): one query row per head, the KV
+// cache split over workgroups, then a log-sum-exp combine.
+//
+// Semantics follow the reference decode kernels
+// (reference: attnfuse/compiler/codegen_decode.py:46-211): per split, an
+// online softmax over its keys gives (m, l, acc); the combine kernel merges
+// m* = max m_s, l* = sum e^(m_s - m*) l_s, O = sum e^(m_s - m*) acc_s / l*.
+// ALiBi uses the query position N_kv - 1: bias = -slope_h |(N_kv-1) - j|
+// (codegen_decode.py:142-145).  Unlike the reference, split boundaries are
+// exact: every key is counted once whatever N_kv is.
+//
+// Work decomposition:
+//  * one workgroup = (split, batch, kv head, chunk of up to 16 query heads
+//    of that kv head's GQA group): the group shares every K/V byte read, so
+//    the cache is streamed once per (batch, kv head) whatever the group size;
+//  * the four waves interleave 32-key steps inside the split; each wave
+//    keeps its own (m, l, O^T) and the waves merge through LDS at the end;
+//  * S^T = K Q^T on the 16x16x32 MFMA with K read straight from HBM into the
+//    A operand (16-byte loads, no LDS); O^T += V^T P^T on the same MFMA with
+//    V^T written to a per-wave LDS tile; P^T feeds the MFMA from registers.
+#pragma once
+
+#include "af_common.hpp"
+
+namespace af {
+
+struct DecodeParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  const float* slopes;
+  float* ws_ml;    // (S, B, Hq, 2) fp32: m (log2 units), l
+  float* ws_acc;   // (S, B, Hq, D) fp32: unnormalised accumulator
+  int64_t qs[4], ks[4], vs[4], os[4];
+  int32_t B, Hq, Hkv, Nkv, G, nqc, nsplit, split_len;
+  float scale;
+};
+
+// 16x16x32 MFMA layouts (lane l, group g = l / 16):
+//   A (16 x 32): row l%16, k-slots 8g..8g+7     B (32 x 16): column l%16
+//   C (16 x 16, 4 fp32): register r holds row 4g + r, column l%16.
+// Two 16-key score blocks give lane (g, q) keys {4g + r} and {16 + 4g + r};
+// those eight values are the B operand of the P*V MFMA over 32 keys when the
+// V^T A operand uses the same key slots: slot e < 4 -> key 4g + e,
+// slot e >= 4 -> key 16 + 4g + (e - 4).
+
+template <class E, int D, int BIAS>
+__global__ void __launch_bounds__(256) decode_split_kernel(const DecodeParams p) {
+  constexpr int KSD = D / 32;      // 32-deep k-steps of K Q^T
+  constexpr int DB = D / 16;       // 16-row blocks of O^T
+  constexpr int VTP = 32 + 8;      // V^T tile pitch (elements)
+  constexpr int VT_ELEMS = D * VTP;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[4 * VT_ELEMS];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int split = blockIdx.x;
+  int rest = blockIdx.y;
+  const int qc = rest % p.nqc; rest /= p.nqc;
+  const int hk = rest % p.Hkv;
+  const int b = rest / p.Hkv;
+  const int hq0 = hk * p.G + 16 * qc;
+  const int nq = min(16, p.G - 16 * qc);   // real query heads in this chunk
+  const int hq = hq0 + c;                  // this lane's query column
+  const bool qreal = c < nq;
+
+  const uint16_t* __restrict__ kbase = p.k + b * p.ks[0] + hk * p.ks[1];
+  const uint16_t* __restrict__ vbase = p.v + b * p.vs[0] + hk * p.vs[1];
+  const int64_t kstr = p.ks[2], vstr = p.vs[2];
+
+  // Q^T as B operand: lane (g, q = c) holds Q[q][32 ks + 8 g .. +7].
+  u32x4 qf[KSD];
+  {
+    const uint16_t* qrow = p.q + b * p.qs[0] + (int64_t)(qreal ? hq : hq0) * p.qs[1];
+#pragma unroll
+    for (int ks = 0; ks < KSD; ++ks)
+      qf[ks] = qreal ? ld16(qrow + 32 * ks + 8 * g) : u32x4{0, 0, 0, 0};
+  }
+  const float c2 = p.scale * kLog2e;
+  float slope2 = 0.f;
+  if constexpr (BIAS == 1) slope2 = qreal ? p.slopes[hq] * kLog2e : 0.f;
+
+  const int s_lo = split * p.split_len;
+  const int s_hi = min(s_lo + p.split_len, p.Nkv);
+  const int nsteps = s_hi > s_lo ? (s_hi - s_lo + 31) / 32 : 0;
+
+  f32x4 o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) o[db] = f32x4{};
+  float m_run = -INFINITY, l_run = 0.f;
+  uint16_t* vt = lds + w * VT_ELEMS;
+  uint32_t* vt32 = reinterpret_cast<uint32_t*>(vt);
+
+  for (int st = w; st < nsteps; st += 4) {
+    const int k0 = s_lo + 32 * st;
+    // K rows for the A operand: block kb covers keys k0 + 16 kb + c.
+    u32x4 ka[2][KSD];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int n = k0 + 16 * kb + c;
+      const bool ok = n < s_hi;
+#pragma unroll
+      for (int ks = 0; ks < KSD; ++ks)
+        ka[kb][ks] = ok ? ld16(kbase + n * kstr + 32 * ks + 8 * g) : u32x4{0, 0, 0, 0};
+    }
+    // V rows: lane owns keys 2c, 2c+1 and 16-byte chunks g + 4 i.
+    u32x4 va[D / 32][2];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      const int dc = g + 4 * i;
+      const int n = k0 + 2 * c;
+      va[i][0] = (n < s_hi) ? ld16(vbase + n * vstr + 8 * dc) : u32x4{0, 0, 0, 0};
+      va[i][1] = (n + 1 < s_hi) ? ld16(vbase + (n + 1) * vstr + 8 * dc) : u32x4{0, 0, 0, 0};
+    }
+    // S^T blocks.
+    f32x4 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      s[kb] = f32x4{};
+#pragma unroll
+      for (int ks = 0; ks < KSD; ++ks) s[kb] = E::mfma16(ka[kb][ks], qf[ks], s[kb]);
+    }
+    // V^T into this wave's LDS tile: row d, column = key - k0.
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      const int dc = g + 4 * i;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t a = va[i][0][e >> 1], bq = va[i][1][e >> 1];
+        const uint32_t word = (e & 1) ? ((a >> 16) | (bq & 0xffff0000u))
+                                      : ((a & 0xffffu) | (bq << 16));
+        vt32[((8 * dc + e) * VTP + 2 * c) >> 1] = word;
+      }
+    }
+    // Online softmax on this lane's eight keys of query c.
+    float x[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = k0 + 16 * kb + 4 * g + r;
+        float v = s[kb][r] * c2;
+        if constexpr (BIAS == 1) v -= slope2 * (float)abs((p.Nkv - 1) - key);
+        v = key < s_hi ? v : -INFINITY;
+        x[4 * kb + r] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    float ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[i] = __builtin_amdgcn_exp2f(x[i] - m_use);
+      ls += x[i];
+    }
+    l_run = l_run * alpha + ls;
+    m_run = m_new;
+    u32x4 pb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pb[i] = E::pack(x[2 * i], x[2 * i + 1]);
+
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const uint16_t* row = vt + (16 * db + c) * VTP + 4 * g;
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(row);
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16);
+      const u32x4 va4 = {lo[0], lo[1], hi[0], hi[1]};
+      o[db] = o[db] * alpha;
+      o[db] = E::mfma16(va4, pb, o[db]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // ---- merge the four waves through LDS ------------------------------------
+  // Per wave: l summed over the four lane groups; m is already uniform.
+  float lw = l_run + __shfl_xor(l_run, 16, 64);
+  lw += __shfl_xor(lw, 32, 64);
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(lds);
+  float* red_m = red;              // [4][16]
+  float* red_l = red + 64;         // [4][16]
+  float* red_o = red + 128;        // [4][16][D]  (q-major)
+  if (g == 0) {
+    red_m[w * 16 + c] = m_run;
+    red_l[w * 16 + c] = lw;
+  }
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red_o[(w * 16 + c) * D + 16 * db + 4 * g + r] = o[db][r];
+  __syncthreads();
+  // 256 threads merge 16 x D outputs.
+  for (int idx = tid; idx < 16 * D; idx += 256) {
+    const int qq = idx / D, d = idx - qq * D;
+    if (qq >= nq) continue;
+    float mstar = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) mstar = fmaxf(mstar, red_m[ww * 16 + qq]);
+    const float mu = (mstar == -INFINITY) ? 0.f : mstar;
+    float acc = 0.f, lsum = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float f = __builtin_amdgcn_exp2f(red_m[ww * 16 + qq] - mu);
+      acc += f * red_o[(ww * 16 + qq) * D + d];
+      lsum += f * red_l[ww * 16 + qq];
+    }
+    const int64_t row = ((int64_t)split * p.B + b) * p.Hq + hq0 + qq;
+    p.ws_acc[row * D + d] = acc;
+    if (d == 0) {
+      p.ws_ml[2 * row] = mstar;
+      p.ws_ml[2 * row + 1] = lsum;
+    }
+  }
+}
+
+// Combine: one wave per (batch, query head); lanes own output dims.
+template <class E, int D>
+__global__ void __launch_bounds__(256) decode_combine_kernel(const DecodeParams p) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);   // b * Hq + hq
+  if (row >= p.B * p.Hq) return;
+  const int b = row / p.Hq, hq = row - b * p.Hq;
+  const int64_t S = p.nsplit;
+  const int64_t plane = (int64_t)p.B * p.Hq;
+  float mstar = -INFINITY;
+  for (int s = 0; s < S; ++s) mstar = fmaxf(mstar, p.ws_ml[2 * (s * plane + row)]);
+  const float mu = (mstar == -INFINITY) ? 0.f : mstar;
+  float lsum = 0.f;
+  constexpr int PER = (D + 63) / 64;
+  float acc[PER] = {};
+  for (int s = 0; s < S; ++s) {
+    const int64_t r = s * plane + row;
+    const float f = __builtin_amdgcn_exp2f(p.ws_ml[2 * r] - mu);
+    lsum += f * p.ws_ml[2 * r + 1];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int d = lane + 64 * i;
+      if (d < D) acc[i] += f * p.ws_acc[r * D + d];
+    }
+  }
+  const float inv = (lsum == 0.f) ? 1.f : 1.f / lsum;
+  uint16_t* orow = p.o + b * p.os[0] + hq * p.os[1];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int d = lane + 64 * i;
+    if (d < D) orow[d] = E::one(acc[i] * inv);
+  }
+}
+
+}  // namespace af

@@ -1,0 +1,86 @@
+// Forward-kernel instantiations for one (dtype, head_dim) pair, selected at
+// compile time with -DAF_DT=<0 f16 | 1 bf16> -DAF_D=<head_dim>.  Splitting
+// the instantiations over several objects keeps each compile short and lets
+// the build run them in parallel.
+#include "launch.hpp"
+
+#ifndef AF_DT
+#error "compile with -DAF_DT=0|1 -DAF_D=<head_dim>"
+#endif
+
+namespace af {
+
+#if AF_DT == 0
+using Elem = F16;
+#define AF_DT_NAME f16
+#else
+using Elem = BF16;
+#define AF_DT_NAME bf16
+#endif
+
+#define AF_FN_(dt, d) launch_fwd_##dt##_d##d
+#define AF_FN(dt, d) AF_FN_(dt, d)
+
+namespace {
+
+template <int MASK, int BIAS, int NORM, bool ROPE, int WAVES>
+int go(const FwdParams& p, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((fwd_kernel<Elem, AF_D, MASK, BIAS, NORM, ROPE, WAVES>),
+                     grid, dim3(64 * WAVES), 0, s, p);
+  return 0;
+}
+
+template <int MASK, int BIAS, int NORM, bool ROPE>
+int pick_waves(const FwdParams& p, int waves, dim3 grid, hipStream_t s) {
+  if constexpr (MASK == MASK_BS) {
+    switch (waves) {
+      case 1: return go<MASK, BIAS, NORM, ROPE, 1>(p, grid, s);
+      case 2: return go<MASK, BIAS, NORM, ROPE, 2>(p, grid, s);
+      case 4: return go<MASK, BIAS, NORM, ROPE, 4>(p, grid, s);
+      default: return -1;
+    }
+  } else {
+    if (waves != 4) return -1;
+    return go<MASK, BIAS, NORM, ROPE, 4>(p, grid, s);
+  }
+}
+
+template <int MASK, int BIAS, int NORM>
+int pick_rope(const FwdParams& p, int rope, int waves, dim3 grid, hipStream_t s) {
+  return rope ? pick_waves<MASK, BIAS, NORM, true>(p, waves, grid, s)
+              : pick_waves<MASK, BIAS, NORM, false>(p, waves, grid, s);
+}
+
+template <int MASK, int BIAS>
+int pick_norm(const FwdParams& p, int norm, int rope, int waves, dim3 grid, hipStream_t s) {
+  switch (norm) {
+    case NORM_SOFTMAX: return pick_rope<MASK, BIAS, NORM_SOFTMAX>(p, rope, waves, grid, s);
+    case NORM_RELU: return pick_rope<MASK, BIAS, NORM_RELU>(p, rope, waves, grid, s);
+    default: return -1;
+  }
+}
+
+template <int MASK>
+int pick_bias(const FwdParams& p, int bias, int norm, int rope, int waves, dim3 grid, hipStream_t s) {
+  switch (bias) {
+    case BIAS_NONE: return pick_norm<MASK, BIAS_NONE>(p, norm, rope, waves, grid, s);
+    case BIAS_ALIBI: return pick_norm<MASK, BIAS_ALIBI>(p, norm, rope, waves, grid, s);
+    case BIAS_ADD: return pick_norm<MASK, BIAS_ADD>(p, norm, rope, waves, grid, s);
+    default: return -1;
+  }
+}
+
+}  // namespace
+
+int AF_FN(AF_DT_NAME, AF_D)(const FwdParams& p, int mask, int bias, int norm,
+                           int rope, int waves, dim3 grid, hipStream_t s) {
+  switch (mask) {
+    case MASK_FULL: return pick_bias<MASK_FULL>(p, bias, norm, rope, waves, grid, s);
+    case MASK_CAUSAL: return pick_bias<MASK_CAUSAL>(p, bias, norm, rope, waves, grid, s);
+    case MASK_SW: return pick_bias<MASK_SW>(p, bias, norm, rope, waves, grid, s);
+    case MASK_BS: return pick_bias<MASK_BS>(p, bias, norm, rope, waves, grid, s);
+    default: return -1;
+  }
+}
+
+}  // namespace af

@@ -1,0 +1,397 @@
+// Fused attention forward for gfx950 (piece (a) + the block-sparse walk of
+// piece (d)).
+//
+// Semantics follow the reference forward kernel
+// (reference: attnfuse/compiler/codegen.py:67-381): S = (rope(q) . rope(k)) *
+// scale, plus ALiBi -slope*|i-j| or an additive bias tile, causal / sliding
+// window / bounds masks, online softmax in fp32 (or ReLU normalised by its
+// row sum), P rounded to the input dtype before P*V, O = acc / l with l == 0
+// treated as 1, optional L = m + ln(l).
+//
+// Work decomposition (MI355X-first, not a translation):
+//  * a workgroup owns BM = 32*WAVES query rows of one (batch, head); each
+//    wave64 owns 32 rows: one 32x32 MFMA output block.
+//  * K and V stream through LDS in 64-key stages, double-buffered: global
+//    loads for stage t+1 are in flight while stage t is on the MFMA pipes.
+//    K is rotated (RoPE) once per stage while it is written to LDS; V is
+//    written transposed (V^T) so that the P*V MFMA reads 16-byte rows.
+//  * scores are computed transposed (S^T = K Q^T): each lane then holds 32
+//    keys of one query, so the row max / row sum are in-register plus one
+//    exchange with lane ^ 32, and P^T is the B operand of the P*V MFMA
+//    without any register shuffle (see af_common.hpp).
+//  * Q stays in registers for the whole kernel, rotated once.
+//  * causal grids run the longest query blocks first.
+#pragma once
+
+#include "af_common.hpp"
+
+namespace af {
+
+enum { MASK_FULL = 0, MASK_CAUSAL = 1, MASK_SW = 2, MASK_BS = 3 };
+enum { BIAS_NONE = 0, BIAS_ALIBI = 1, BIAS_ADD = 2 };
+enum { NORM_SOFTMAX = 0, NORM_RELU = 1 };
+
+struct FwdParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  float* lse;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  const float* slopes;
+  const uint16_t* bias;
+  uint32_t* coverage;
+  const int32_t* bs_full_num;
+  const int32_t* bs_full_idx;
+  const int32_t* bs_part_num;
+  const int32_t* bs_part_idx;
+  int64_t qs[4], ks[4], vs[4], os[4], ls[3], rs[2], bs[4];
+  int64_t bs_full_rs, bs_part_rs;
+  int32_t B, Hq, Hkv, Nq, Nkv, G;
+  int32_t n_mblocks, bs_block_n;
+  int32_t cov_nq, cov_nk;
+  float scale;
+  int32_t window;
+};
+
+template <class E, int D, int MASK, int BIAS, int NORM, bool ROPE, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64)
+    fwd_kernel(const FwdParams p) {
+  constexpr int NT = WAVES * 64;
+  constexpr int BM = 32 * WAVES;
+  constexpr int BN = 64;
+  constexpr int KP = D + 8;    // K stage row pitch (elements)
+  constexpr int VP = BN + 8;   // V^T stage row pitch (elements)
+  constexpr int KS = D / 16;   // 16-deep k-steps of Q K^T
+  constexpr int DB = D / 32;   // 32-row blocks of O^T
+  constexpr int STAGE = BN * KP + D * VP;  // elements per LDS stage
+  // K staging: rotate-half pairs (chunk j, chunk j + D/16) of one key row.
+  constexpr int KPAIRS = BN * D / 16;
+  constexpr int KPT = (KPAIRS + NT - 1) / NT;
+  // V staging: units of 2 keys x 8 dims, written to V^T as packed pairs.
+  constexpr int VUNITS = (BN / 2) * (D / 8);
+  constexpr int VPT = (VUNITS + NT - 1) / NT;
+
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int h = lane >> 5;
+  const int c = lane & 31;
+
+  const int BH = p.B * p.Hq;
+  const int bh = blockIdx.x % BH;
+  const int mbi = blockIdx.x / BH;
+  const int mb = (MASK == MASK_CAUSAL) ? (p.n_mblocks - 1 - mbi) : mbi;
+  const int b = bh / p.Hq;
+  const int hq = bh - b * p.Hq;
+  const int hk = hq / p.G;
+  const int m0 = mb * BM;
+  const int q0w = m0 + 32 * w;
+  const int qrow = q0w + c;
+
+  const uint16_t* __restrict__ qbase = p.q + b * p.qs[0] + hq * p.qs[1];
+  const uint16_t* __restrict__ kbase = p.k + b * p.ks[0] + hk * p.ks[1];
+  const uint16_t* __restrict__ vbase = p.v + b * p.vs[0] + hk * p.vs[1];
+  const int64_t kstr = p.ks[2], vstr = p.vs[2];
+  const int64_t rstr = p.rs[0];
+
+  // ---- Q fragment (B operand of S^T = K Q^T), rotated once -------------
+  u32x4 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    qf[ks] = (qrow < p.Nq) ? ld16(qbase + qrow * p.qs[2] + 16 * ks + 8 * h)
+                           : u32x4{0, 0, 0, 0};
+  }
+  if constexpr (ROPE) {
+    if (qrow < p.Nq) {
+      const uint16_t* cr = p.cos + qrow * rstr;
+      const uint16_t* sr = p.sin + qrow * rstr;
+#pragma unroll
+      for (int ks = 0; ks < KS / 2; ++ks) {
+        const int dl = 16 * ks + 8 * h, dh = dl + D / 2;
+        rope_pair<E>(qf[ks], qf[ks + KS / 2], ld16(cr + dl), ld16(sr + dl),
+                     ld16(cr + dh), ld16(sr + dh));
+      }
+    }
+  }
+
+  // ---- key-tile schedule ------------------------------------------------
+  int n_lo = 0, n_hi = p.Nkv, ntiles;
+  int bs_nfull = 0, bs_sub = 1;
+  const int32_t* bs_full_row = nullptr;
+  const int32_t* bs_part_row = nullptr;
+  if constexpr (MASK == MASK_CAUSAL) {
+    n_hi = min(m0 + BM, p.Nkv);
+  } else if constexpr (MASK == MASK_SW) {
+    n_lo = max(m0 - p.window + 1, 0) & ~(BN - 1);
+    n_hi = min(m0 + BM - 1 + p.window, p.Nkv);
+  }
+  if constexpr (MASK == MASK_BS) {
+    bs_sub = p.bs_block_n / BN;
+    bs_nfull = p.bs_full_num[mb];
+    bs_full_row = p.bs_full_idx + mb * p.bs_full_rs;
+    bs_part_row = p.bs_part_idx + mb * p.bs_part_rs;
+    ntiles = (bs_nfull + p.bs_part_num[mb]) * bs_sub;
+  } else {
+    ntiles = n_hi > n_lo ? (n_hi - n_lo + BN - 1) / BN : 0;
+  }
+  auto tile_n0 = [&](int t) -> int {
+    if constexpr (MASK == MASK_BS) {
+      const int e = t / bs_sub, s = t - e * bs_sub;
+      const int blk = e < bs_nfull ? bs_full_row[e] : bs_part_row[e - bs_nfull];
+      return blk * p.bs_block_n + s * BN;
+    } else {
+      return n_lo + t * BN;
+    }
+  };
+
+  // ---- staging registers --------------------------------------------------
+  u32x4 kr[KPT][2];
+  u32x4 kc[ROPE ? KPT : 1][2], ksn[ROPE ? KPT : 1][2];
+  u32x4 vr[VPT][2];
+
+  auto stage_load = [&](int n0) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int pi = tid + i * NT;
+      const int row = pi / (D / 16), j = pi % (D / 16);
+      const int n = n0 + row;
+      const bool ok = (KPAIRS % NT == 0 || pi < KPAIRS) && n >= 0 && n < p.Nkv;
+      const uint16_t* kp = kbase + n * kstr + 8 * j;
+      kr[i][0] = ok ? ld16(kp) : u32x4{0, 0, 0, 0};
+      kr[i][1] = ok ? ld16(kp + D / 2) : u32x4{0, 0, 0, 0};
+      if constexpr (ROPE) {
+        const uint16_t* cp = p.cos + n * rstr + 8 * j;
+        const uint16_t* sp = p.sin + n * rstr + 8 * j;
+        kc[i][0] = ok ? ld16(cp) : u32x4{0, 0, 0, 0};
+        kc[i][1] = ok ? ld16(cp + D / 2) : u32x4{0, 0, 0, 0};
+        ksn[i][0] = ok ? ld16(sp) : u32x4{0, 0, 0, 0};
+        ksn[i][1] = ok ? ld16(sp + D / 2) : u32x4{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int u = tid + i * NT;
+      const int dc = u % (D / 8), kg = u / (D / 8);
+      const int n = n0 + 2 * kg;
+      const bool ok = VUNITS % NT == 0 || u < VUNITS;
+      const uint16_t* vp = vbase + n * vstr + 8 * dc;
+      vr[i][0] = (ok && n >= 0 && n < p.Nkv) ? ld16(vp) : u32x4{0, 0, 0, 0};
+      vr[i][1] = (ok && n >= 0 && n + 1 < p.Nkv) ? ld16(vp + vstr) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto stage_store = [&](uint16_t* buf) {
+    uint16_t* Ks = buf;
+    uint16_t* Vt = buf + BN * KP;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int pi = tid + i * NT;
+      if (KPAIRS % NT == 0 || pi < KPAIRS) {
+        const int row = pi / (D / 16), j = pi % (D / 16);
+        u32x4 lo = kr[i][0], hi = kr[i][1];
+        if constexpr (ROPE) rope_pair<E>(lo, hi, kc[i][0], ksn[i][0], kc[i][1], ksn[i][1]);
+        st16(Ks + row * KP + 8 * j, lo);
+        st16(Ks + row * KP + 8 * j + D / 2, hi);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int u = tid + i * NT;
+      if (VUNITS % NT == 0 || u < VUNITS) {
+        const int dc = u % (D / 8), kg = u / (D / 8);
+        uint32_t* vt32 = reinterpret_cast<uint32_t*>(Vt);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t a = vr[i][0][e >> 1], bq = vr[i][1][e >> 1];
+          const uint32_t word = (e & 1) ? ((a >> 16) | (bq & 0xffff0000u))
+                                        : ((a & 0xffffu) | (bq << 16));
+          vt32[((8 * dc + e) * VP + 2 * kg) >> 1] = word;
+        }
+      }
+    }
+  };
+
+  // ---- online-softmax state ------------------------------------------------
+  f32x16 o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) o[db] = f32x16{};
+  float m_run = -INFINITY;   // running max, log2 units (softmax)
+  float l_run = 0.f;         // this lane's half of the row sum
+  const float c2 = p.scale * kLog2e;
+  float slope2 = 0.f;
+  if constexpr (BIAS == BIAS_ALIBI) slope2 = p.slopes[hq] * kLog2e;
+  const uint16_t* brow = nullptr;
+  if constexpr (BIAS == BIAS_ADD) brow = p.bias + b * p.bs[0] + hq * p.bs[1] + (int64_t)qrow * p.bs[2];
+
+  if (ntiles > 0) {
+    stage_load(tile_n0(0));
+    stage_store(lds);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int n0 = tile_n0(t);
+    const bool more = t + 1 < ntiles;
+    if (more) stage_load(tile_n0(t + 1));
+    const uint16_t* Ks = lds + (t & 1) * STAGE;
+    const uint16_t* Vt = Ks + BN * KP;
+
+    bool active = q0w < p.Nq && n0 >= 0 && n0 < p.Nkv;
+    if constexpr (MASK == MASK_CAUSAL) active = active && n0 <= q0w + 31;
+    if constexpr (MASK == MASK_SW)
+      active = active && n0 + BN - 1 > q0w - p.window && n0 < q0w + 31 + p.window;
+
+    if (active) {
+      if (p.coverage != nullptr && lane == 0) {
+        const int64_t ci = ((int64_t)(b * p.Hq + hq) * p.cov_nq + (q0w >> 5)) * p.cov_nk + (n0 >> 6);
+        atomicAdd(p.coverage + ci, 1u);
+      }
+      // S^T = K Q^T over this stage: two 32-key blocks.
+      f32x16 s[BN / 32];
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb) {
+        s[kb] = f32x16{};
+        const uint16_t* krow = Ks + (32 * kb + kperm(c)) * KP + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          s[kb] = E::mfma32(ld16(krow + 16 * ks), qf[ks], s[kb]);
+      }
+
+      bool need_mask = n0 + BN > p.Nkv;
+      if constexpr (MASK == MASK_CAUSAL) need_mask = need_mask || n0 + BN - 1 > q0w;
+      if constexpr (MASK == MASK_SW)
+        need_mask = need_mask || (q0w + 31 - n0 >= p.window) || (n0 + BN - 1 - q0w >= p.window);
+
+      // scores -> log2-domain logits (softmax) or natural logits (relu)
+      const float cs = (NORM == NORM_SOFTMAX) ? c2 : p.scale;
+      const float bscale = (NORM == NORM_SOFTMAX) ? kLog2e : 1.f;
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb) {
+        if constexpr (BIAS == BIAS_ADD) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int key0 = n0 + 32 * kb + 16 * j + 8 * h;
+            float bv[8];
+            if (qrow < p.Nq && key0 + 8 <= p.Nkv) {
+              unpack8<E>(ld16(brow + key0 * p.bs[3]), bv);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const uint16_t raw = (qrow < p.Nq && key0 + e < p.Nkv) ? brow[(key0 + e) * p.bs[3]] : 0;
+                bv[e] = E::lo(raw);
+              }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[kb][8 * j + e] = s[kb][8 * j + e] * cs + bv[e] * bscale;
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[kb][r] *= cs;
+        }
+        if constexpr (BIAS == BIAS_ALIBI) {
+          const float sl = (NORM == NORM_SOFTMAX) ? slope2 : slope2 * kLn2;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = n0 + 32 * kb + acc_key(r, h);
+            s[kb][r] -= sl * (float)abs(qrow - key);
+          }
+        }
+        if (need_mask) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = n0 + 32 * kb + acc_key(r, h);
+            bool ok = key < p.Nkv;
+            if constexpr (MASK == MASK_CAUSAL) ok = ok && key <= qrow;
+            if constexpr (MASK == MASK_SW) ok = ok && abs(qrow - key) < p.window;
+            s[kb][r] = ok ? s[kb][r] : -INFINITY;
+          }
+        }
+      }
+
+      float alpha = 1.f;
+      if constexpr (NORM == NORM_SOFTMAX) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+        mx = fmaxf(mx, xor32(mx));
+        const float m_new = fmaxf(m_run, mx);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        float ls = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float pv = __builtin_amdgcn_exp2f(s[kb][r] - m_use);
+            s[kb][r] = pv;
+            ls += pv;
+          }
+        l_run = l_run * alpha + ls;
+        m_run = m_new;
+      } else {
+        float ls = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float pv = fmaxf(s[kb][r], 0.f);
+            s[kb][r] = pv;
+            ls += pv;
+          }
+        l_run += ls;
+      }
+
+      // P^T (registers) -> B operands, one per 16 keys.
+      u32x4 pf[BN / 16];
+#pragma unroll
+      for (int kk = 0; kk < BN / 16; ++kk) {
+        const int kb = kk >> 1, j = kk & 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          pf[kk][i] = E::pack(s[kb][8 * j + 2 * i], s[kb][8 * j + 2 * i + 1]);
+      }
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        if constexpr (NORM == NORM_SOFTMAX) o[db] *= alpha;
+        const uint16_t* vrow = Vt + (32 * db + c) * VP + 8 * h;
+#pragma unroll
+        for (int kk = 0; kk < BN / 16; ++kk)
+          o[db] = E::mfma32(ld16(vrow + 16 * kk), pf[kk], o[db]);
+      }
+    }
+
+    if (more) stage_store(lds + ((t + 1) & 1) * STAGE);
+    __syncthreads();
+  }
+
+  // ---- epilogue -------------------------------------------------------------
+  const float lt = l_run + xor32(l_run);
+  const float inv = (lt == 0.f) ? 1.f : 1.f / lt;
+  if (qrow < p.Nq) {
+    uint16_t* orow = p.o + b * p.os[0] + hq * p.os[1] + (int64_t)qrow * p.os[2];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = 32 * db + 8 * g + 4 * h;
+        u32x2 w2;
+        w2[0] = E::pack(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
+        w2[1] = E::pack(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + d0) = w2;
+      }
+    if (p.lse != nullptr && h == 0) {
+      const float ll = (lt == 0.f) ? 1.f : lt;
+      float L;
+      if constexpr (NORM == NORM_SOFTMAX) L = (m_run + __log2f(ll)) * kLn2;
+      else L = -INFINITY;
+      p.lse[b * p.ls[0] + hq * p.ls[1] + (int64_t)qrow * p.ls[2]] = L;
+    }
+  }
+}
+
+}  // namespace af

@@ -1,0 +1,29 @@
+// Host-side launch helpers shared by the instantiation units and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fwd_kernel.hpp"
+
+namespace af {
+
+// Thread-local error text behind af_last_error().
+void set_error(const char* fmt, ...);
+
+// Per-(dtype, head_dim) forward launchers, defined in fwd_inst.hip (one
+// object per pair).  `waves` is the workgroup width (32 query rows per wave).
+// Return 0, or AF_ERR_UNSUPPORTED when the pair has no instantiation for the
+// (mask, bias, norm, rope, waves) combination.
+#define AF_DECLARE_FWD(NAME) \
+  int NAME(const FwdParams& p, int mask, int bias, int norm, int rope, \
+           int waves, dim3 grid, hipStream_t stream);
+AF_DECLARE_FWD(launch_fwd_f16_d32)
+AF_DECLARE_FWD(launch_fwd_f16_d64)
+AF_DECLARE_FWD(launch_fwd_f16_d128)
+AF_DECLARE_FWD(launch_fwd_bf16_d32)
+AF_DECLARE_FWD(launch_fwd_bf16_d64)
+AF_DECLARE_FWD(launch_fwd_bf16_d128)
+#undef AF_DECLARE_FWD
+
+}  // namespace af

@@ -1,0 +1,95 @@
+"""Backward route: (Q, K, V, O, L, dO) -> (dQ, dK, dV) via ``af_bwd``.
+
+Keeps the reference signatures (reference: attnfuse/runtime/backward.py:69-192)
+and widens the scope the reference accepts ({full, causal} x {none, ALiBi},
+no RoPE) to softmax graphs with full, causal, sliding-window or block-sparse
+masks, no bias or ALiBi, with or without fused RoPE.  With RoPE the kernels
+differentiate through the rotation, so dQ/dK are gradients with respect to
+the un-rotated inputs.  dK/dV of a GQA key/value head are summed over its
+query-head group inside the kernel (no atomics).
+"""
+from __future__ import annotations
+
+import torch
+
+from ..ir.high_level import BiasKind, Graph, MaskKind, NormKind
+from . import _native as N
+
+_MASK_CODES = {MaskKind.FULL: 0, MaskKind.CAUSAL: 1,
+               MaskKind.SLIDING_WINDOW: 2, MaskKind.BLOCK_SPARSE: 3}
+
+
+def can_backward(graph: Graph) -> bool:
+    if graph.norm().kind is not NormKind.SOFTMAX:
+        return False
+    masks = {m.kind for m in graph.collect_masks()}
+    if masks - set(_MASK_CODES):
+        return False
+    if {b.kind for b in graph.collect_biases()} - {BiasKind.ALIBI}:
+        return False
+    return True
+
+
+def _bwd_workspace(device, nbytes: int) -> torch.Tensor:
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+def _run_backward_key(key, Q, K, V, O, L, dO, sm_scale, window, cos, sin,
+                      block_mask, alibi_slopes):
+    from .dispatch import _slopes_f32, check_qkv, kernel_layout, rope_tables
+    check_qkv(Q, K, V)
+    B, Hq, Nq, D = Q.shape
+    Hkv, Nkv = K.shape[1], K.shape[2]
+    if L.shape != (B, Hq, Nq) or L.dtype != torch.float32:
+        raise ValueError("L must be the (B, H_q, N_q) float32 log-sum-exp")
+    Qk, Kk, Vk = kernel_layout(Q), kernel_layout(K), kernel_layout(V)
+    Ok, dOk = kernel_layout(O), kernel_layout(dO.to(Q.dtype))
+    dQ = torch.empty_like(Qk)
+    dK = torch.empty_like(Kk)
+    dV = torch.empty_like(Vk)
+    slopes = _slopes_f32(Hq, Q, alibi_slopes) if key[3] == 1 else None
+    c = s = None
+    if key[5]:
+        c, s = rope_tables(cos, sin, Q)
+    a = N.BwdArgsC()
+    a.key = N.SpecKeyC(*key)
+    a.q, a.k, a.v = Qk.data_ptr(), Kk.data_ptr(), Vk.data_ptr()
+    a.o, a.dout, a.lse = Ok.data_ptr(), dOk.data_ptr(), L.data_ptr()
+    a.dq, a.dk, a.dv = dQ.data_ptr(), dK.data_ptr(), dV.data_ptr()
+    a.cos, a.sin = N.ptr(c), N.ptr(s)
+    a.alibi_slopes = N.ptr(slopes)
+    a.q_stride[:] = Qk.stride()
+    a.k_stride[:] = Kk.stride()
+    a.v_stride[:] = Vk.stride()
+    a.o_stride[:] = Ok.stride()
+    a.do_stride[:] = dOk.stride()
+    a.dq_stride[:] = dQ.stride()
+    a.dk_stride[:] = dK.stride()
+    a.dv_stride[:] = dV.stride()
+    a.lse_stride[:] = L.stride()
+    a.rope_stride[:] = N.strides(c, 2)
+    a.batch, a.heads_q, a.heads_kv = B, Hq, Hkv
+    a.seqlen_q, a.seqlen_kv = Nq, Nkv
+    a.rope_len = 0 if c is None else c.shape[0]
+    a.scale = float(sm_scale)
+    a.window = int(window or 0)
+    nbytes = int(N.lib().af_bwd_workspace_bytes(B, Hq, Nq))
+    ws = _bwd_workspace(Q.device, nbytes)
+    bm = block_mask._c() if block_mask is not None else None
+    N.check(N.lib().af_bwd(a, bm, ws.data_ptr(), ws.numel(),
+                           N.stream_handle(Q.device)))
+    return dQ, dK, dV
+
+
+def run_backward(graph: Graph, Q: torch.Tensor, K: torch.Tensor,
+                 V: torch.Tensor, O: torch.Tensor, L: torch.Tensor,
+                 dO: torch.Tensor, sm_scale: float, *, cos=None, sin=None,
+                 block_mask=None, alibi_slopes=None) -> tuple:
+    """Return (dQ, dK, dV) for a graph inside ``can_backward``'s scope."""
+    from .kernel_cache import get_or_compile
+    if not can_backward(graph):
+        raise NotImplementedError("graph is outside the backward scope")
+    bundle = get_or_compile(graph)
+    key = bundle.key.abi_tuple()
+    return _run_backward_key(key, Q, K, V, O, L, dO, sm_scale, bundle.window,
+                             cos, sin, block_mask, alibi_slopes)

@@ -1,0 +1,202 @@
+"""Block-sparse masks: the ``BlockMask`` CSR format, its construction, and
+the block-sparse forward/backward launches.
+
+``BlockMask`` keeps the reference's fields and semantics (reference:
+attnfuse/runtime/block_mask.py:74-202): Q-major lists of active key blocks
+(``full_kv_*``; the ``kv_*`` partial lists stay empty because a tile with any
+active element is rounded up to fully active), a K-major transpose
+(``q_*``) for the dK/dV backward, zero-padded int32 rows of width
+``max(1, longest row)``, indices ascending.
+
+``create_block_mask`` evaluates the predicate on the (Q_LEN, KV_LEN) index
+grid exactly like the reference, but reduces it to the block grid with one
+reshape + ``any`` instead of a Python loop over tiles.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Callable, Optional
+
+import torch
+
+from . import _native as N
+
+
+@dataclass
+class BlockMask:
+    kv_num_blocks: torch.Tensor   # (n_q_blocks,) int32, partial tiles
+    kv_indices: torch.Tensor      # (n_q_blocks, max_partial) int32
+    full_kv_num: torch.Tensor     # (n_q_blocks,) int32
+    full_kv_idx: torch.Tensor     # (n_q_blocks, max_full) int32
+    q_num_blocks: torch.Tensor    # (n_kv_blocks,) int32
+    q_indices: torch.Tensor       # (n_kv_blocks, max_q) int32
+    BLOCK_M: int
+    BLOCK_N: int
+    n_q_blocks: int
+    n_kv_blocks: int
+    n_active: int
+    n_full: int
+
+    def to(self, device) -> "BlockMask":
+        f = {k: (v.to(device) if isinstance(v, torch.Tensor) else v)
+             for k, v in self.__dict__.items()}
+        return BlockMask(**f)
+
+    def dense_blocks(self) -> torch.Tensor:
+        """(n_q_blocks, n_kv_blocks) bool grid of visited tiles."""
+        grid = torch.zeros(self.n_q_blocks, self.n_kv_blocks, dtype=torch.bool)
+        for num, idx in ((self.full_kv_num, self.full_kv_idx),
+                         (self.kv_num_blocks, self.kv_indices)):
+            num, idx = num.cpu(), idx.cpu()
+            for r in range(self.n_q_blocks):
+                grid[r, idx[r, : int(num[r])].long()] = True
+        return grid
+
+    def _c(self) -> "N.BlockMaskC":
+        bm = N.BlockMaskC()
+        bm.full_kv_num = self.full_kv_num.data_ptr()
+        bm.full_kv_idx = self.full_kv_idx.data_ptr()
+        bm.kv_num_blocks = self.kv_num_blocks.data_ptr()
+        bm.kv_indices = self.kv_indices.data_ptr()
+        bm.q_num_blocks = self.q_num_blocks.data_ptr()
+        bm.q_indices = self.q_indices.data_ptr()
+        bm.full_kv_stride = self.full_kv_idx.stride(0)
+        bm.kv_stride = self.kv_indices.stride(0)
+        bm.q_stride = self.q_indices.stride(0)
+        bm.block_m, bm.block_n = self.BLOCK_M, self.BLOCK_N
+        bm.n_q_blocks, bm.n_kv_blocks = self.n_q_blocks, self.n_kv_blocks
+        return bm
+
+
+def _csr_rows(active: torch.Tensor):
+    """Padded ascending index rows of a bool grid: (counts, indices)."""
+    counts = active.sum(dim=1).to(torch.int32)
+    width = max(1, int(counts.max()) if counts.numel() else 1)
+    # a stable sort of ~active puts the active columns first, ascending
+    order = torch.sort((~active).to(torch.int8), dim=1, stable=True).indices
+    idx = order[:, :width].to(torch.int32)
+    keep = torch.arange(width)[None, :] < counts[:, None].long()
+    idx = torch.where(keep, idx, torch.zeros_like(idx))
+    return counts, idx.contiguous()
+
+
+def block_mask_from_blocks(active: torch.Tensor, BLOCK_M: int, BLOCK_N: int,
+                           device="cuda") -> BlockMask:
+    """Build a BlockMask from a (n_q_blocks, n_kv_blocks) bool tile grid."""
+    active = active.to(torch.bool).cpu()
+    nqb, nkb = active.shape
+    full_num, full_idx = _csr_rows(active)
+    q_num, q_idx = _csr_rows(active.t().contiguous())
+    empty_num = torch.zeros(nqb, dtype=torch.int32)
+    empty_idx = torch.zeros(nqb, 1, dtype=torch.int32)
+    n = int(full_num.sum())
+    return BlockMask(
+        kv_num_blocks=empty_num.to(device), kv_indices=empty_idx.to(device),
+        full_kv_num=full_num.to(device), full_kv_idx=full_idx.to(device),
+        q_num_blocks=q_num.to(device), q_indices=q_idx.to(device),
+        BLOCK_M=BLOCK_M, BLOCK_N=BLOCK_N, n_q_blocks=nqb, n_kv_blocks=nkb,
+        n_active=n, n_full=n)
+
+
+def create_block_mask(mask_fn: Callable, Q_LEN: int, KV_LEN: int,
+                      BLOCK_M: int = 64, BLOCK_N: int = 64,
+                      device="cuda") -> BlockMask:
+    """BlockMask from an element predicate ``mask_fn(q_idx, kv_idx) -> bool``
+    evaluated on (Q_LEN, KV_LEN) index grids.  A tile with any True element
+    is active (and visited whole)."""
+    nqb = (Q_LEN + BLOCK_M - 1) // BLOCK_M
+    nkb = (KV_LEN + BLOCK_N - 1) // BLOCK_N
+    qi = torch.arange(Q_LEN)[:, None].expand(Q_LEN, KV_LEN)
+    kj = torch.arange(KV_LEN)[None, :].expand(Q_LEN, KV_LEN)
+    elem = torch.as_tensor(mask_fn(qi, kj), dtype=torch.bool)
+    elem = elem.expand(Q_LEN, KV_LEN)
+    padded = torch.zeros(nqb * BLOCK_M, nkb * BLOCK_N, dtype=torch.bool)
+    padded[:Q_LEN, :KV_LEN] = elem
+    active = padded.view(nqb, BLOCK_M, nkb, BLOCK_N).any(dim=3).any(dim=1)
+    return block_mask_from_blocks(active, BLOCK_M, BLOCK_N, device)
+
+
+def _check_mask(Q, K, bm: BlockMask) -> None:
+    if not isinstance(bm, BlockMask):
+        raise TypeError("block_mask must be an attnfuse.BlockMask")
+    if bm.full_kv_idx.device != Q.device:
+        raise ValueError("block_mask lives on another device than Q; call "
+                         "block_mask.to(Q.device)")
+    nqb = (Q.shape[2] + bm.BLOCK_M - 1) // bm.BLOCK_M
+    nkb = (K.shape[2] + bm.BLOCK_N - 1) // bm.BLOCK_N
+    if (nqb, nkb) != (bm.n_q_blocks, bm.n_kv_blocks):
+        raise ValueError(f"block_mask grid {bm.n_q_blocks}x{bm.n_kv_blocks} "
+                         f"does not fit N_q={Q.shape[2]}, N_kv={K.shape[2]}")
+
+
+def _bs_key(Q, bias_kind: int, rope: bool):
+    dt = {torch.float16: 0, torch.bfloat16: 1}.get(Q.dtype)
+    if dt is None:
+        raise NotImplementedError(f"block-sparse kernels take fp16/bf16, "
+                                  f"got {Q.dtype}")
+    return (dt, Q.shape[-1], 3, int(bias_kind), 0, int(rope))
+
+
+def run_block_sparse(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
+                     block_mask: BlockMask, sm_scale: float,
+                     bias_kind: int = 0, out: Optional[torch.Tensor] = None,
+                     save_lse: Optional[torch.Tensor] = None, *,
+                     cos=None, sin=None, alibi_slopes=None,
+                     coverage: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Block-sparse forward (reference signature,
+    attnfuse/runtime/block_mask.py:205-210).  ``bias_kind`` 1 = ALiBi.
+    ``cos``/``sin`` apply fused RoPE."""
+    from .dispatch import (_rows_ok, _slopes_f32, check_qkv, fill_fwd_args,
+                           kernel_layout, rope_tables)
+    check_qkv(Q, K, V)
+    _check_mask(Q, K, block_mask)
+    B, H, Nq, D = Q.shape
+    rope = cos is not None or sin is not None
+    key = _bs_key(Q, bias_kind, rope)
+    if out is None:
+        out = torch.empty_like(Q)
+    slopes = _slopes_f32(H, Q, alibi_slopes) if bias_kind == 1 else None
+    c = s = None
+    if rope:
+        c, s = rope_tables(cos, sin, Q)
+    Qk, Kk, Vk = kernel_layout(Q), kernel_layout(K), kernel_layout(V)
+    o = out if _rows_ok(out) else torch.empty_like(Q)
+    a = N.FwdArgsC()
+    fill_fwd_args(a, key, Qk, Kk, Vk, o, save_lse, c, s, slopes, None,
+                  coverage, sm_scale, 0)
+    bm = block_mask._c()
+    N.check(N.lib().af_fwd_blocksparse(a, bm, N.stream_handle(Q.device)))
+    if o is not out:
+        out.copy_(o)
+    return out
+
+
+def run_block_sparse_graph(graph, Q, K, V, block_mask: BlockMask, *, cos=None,
+                           sin=None, out=None, save_lse=None):
+    """Block-sparse forward of a traced graph, honouring its scale, ALiBi and
+    RoPE."""
+    from .kernel_cache import get_or_compile
+    bundle = get_or_compile(graph)
+    if bundle.bias_kind == 2:
+        raise NotImplementedError("additive bias with block_sparse is not "
+                                  "supported")
+    if bundle.has_rope and (cos is None or sin is None):
+        raise RuntimeError("this graph uses af.rope(); pass cos= and sin=")
+    return run_block_sparse(Q, K, V, block_mask, bundle.sm_scale,
+                            bias_kind=bundle.bias_kind, out=out,
+                            save_lse=save_lse,
+                            cos=cos if bundle.has_rope else None,
+                            sin=sin if bundle.has_rope else None)
+
+
+def run_block_sparse_backward(Q, K, V, O, L, dO, block_mask: BlockMask,
+                              sm_scale: float, bias_kind: int = 0, *,
+                              cos=None, sin=None, alibi_slopes=None):
+    """Block-sparse backward -> (dQ, dK, dV) (reference signature,
+    attnfuse/runtime/block_mask.py:274-275)."""
+    from .backward import _run_backward_key
+    _check_mask(Q, K, block_mask)
+    rope = cos is not None or sin is not None
+    key = _bs_key(Q, bias_kind, rope)
+    return _run_backward_key(key, Q, K, V, O, L, dO, sm_scale, 0, cos, sin,
+                             block_mask, alibi_slopes)

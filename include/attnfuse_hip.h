@@ -1,0 +1,195 @@
+/*
+ * attnfuse_hip.h -- C ABI of libattnfuse_hip.so, the MI355X (gfx950) kernels
+ * behind the AttnFuse attention DSL.
+ *
+ * The reference launches Triton kernels straight from Python
+ * (reference: attnfuse/runtime/dispatch.py:196-214,
+ * attnfuse/runtime/flash_decode.py:150-186, attnfuse/runtime/backward.py:130-190,
+ * attnfuse/runtime/block_mask.py:244-269,299-363).  This header is the
+ * boundary that replaces those launch sites: plain C, plain pointers, element
+ * strides and sizes, no torch or HIP types.  Any FFI (ctypes, cffi, a C++
+ * extension) can bind it.
+ *
+ * Contract
+ *  - The library never allocates or frees device memory.  Outputs and
+ *    workspaces are caller-owned.
+ *  - Tensors are (B, H, N, D) with arbitrary element strides, except that
+ *    the innermost (head-dim) stride must be 1, base pointers must be 16-byte
+ *    aligned and the batch/head/sequence strides must be multiples of 8
+ *    elements (16-byte rows for 16-byte vector loads).
+ *  - Every launch goes on the caller's stream (a hipStream_t passed as
+ *    void*; NULL is the legacy default stream).  Launches are asynchronous.
+ *  - Return value: AF_OK (0) when the kernels were enqueued; a negative
+ *    af_status otherwise, with a message in af_last_error() (thread-local).
+ *  - Reentrant: no mutable global state besides the immutable kernel table.
+ */
+#ifndef ATTNFUSE_HIP_H
+#define ATTNFUSE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AF_ABI_VERSION 1
+
+typedef enum af_status {
+  AF_OK = 0,
+  AF_ERR_UNSUPPORTED = -1, /* no instantiation for this specialisation key */
+  AF_ERR_BAD_ARG = -2,     /* shape, stride, alignment or pointer problem  */
+  AF_ERR_LAUNCH = -3,      /* the HIP runtime refused the launch           */
+  AF_ERR_WORKSPACE = -4    /* workspace missing or too small               */
+} af_status;
+
+typedef enum af_dtype { AF_F16 = 0, AF_BF16 = 1, AF_F32 = 2 } af_dtype;
+
+/* Mask kinds (reference MASK_KIND encoding, attnfuse/compiler/codegen.py:88,
+ * extended with the block-sparse kind). */
+typedef enum af_mask {
+  AF_MASK_FULL = 0,
+  AF_MASK_CAUSAL = 1,          /* key j visible to query i iff j <= i        */
+  AF_MASK_SLIDING_WINDOW = 2,  /* visible iff |i - j| < window               */
+  AF_MASK_BLOCK_SPARSE = 3     /* visible iff (i/BM, j/BN) is a listed tile  */
+} af_mask;
+
+typedef enum af_bias {
+  AF_BIAS_NONE = 0,
+  AF_BIAS_ALIBI = 1,    /* S += -slope[h] * |i - j|; decode: |(N_kv-1) - j| */
+  AF_BIAS_ADDITIVE = 2  /* S += bias[b][h][i][j]                             */
+} af_bias;
+
+typedef enum af_norm { AF_NORM_SOFTMAX = 0, AF_NORM_RELU = 1 } af_norm;
+
+/* Specialisation key: replaces the reference's Triton constexpr record
+ * (attnfuse/compiler/codegen.py:391-404; attnfuse/ir/tiled.py:52-81). */
+typedef struct af_spec_key {
+  int32_t dtype;     /* af_dtype                  */
+  int32_t head_dim;  /* 32, 64, 96, 128 or 256    */
+  int32_t mask;      /* af_mask                   */
+  int32_t bias;      /* af_bias                   */
+  int32_t norm;      /* af_norm                   */
+  int32_t rope;      /* 1: rotate-half RoPE fused */
+} af_spec_key;
+
+/* Block-sparse mask in CSR form: the reference BlockMask fields
+ * (attnfuse/runtime/block_mask.py:84-97).  Row r of the Q-major lists names
+ * the key blocks query block r visits; the K-major lists are the transpose
+ * (used by the dK/dV backward).  All arrays are device int32. */
+typedef struct af_blockmask {
+  const int32_t* full_kv_num;   /* (n_q_blocks)                 */
+  const int32_t* full_kv_idx;   /* (n_q_blocks, full_kv_stride) */
+  const int32_t* kv_num_blocks; /* (n_q_blocks) partial tiles   */
+  const int32_t* kv_indices;    /* (n_q_blocks, kv_stride)      */
+  const int32_t* q_num_blocks;  /* (n_kv_blocks)                */
+  const int32_t* q_indices;     /* (n_kv_blocks, q_stride)      */
+  int64_t full_kv_stride, kv_stride, q_stride;
+  int32_t block_m, block_n, n_q_blocks, n_kv_blocks;
+} af_blockmask;
+
+/* Forward attention.  Replaces the attnfuse_fwd_kernel launch
+ * (reference: attnfuse/runtime/dispatch.py:69-215, kernel
+ * attnfuse/compiler/codegen.py:67-381). */
+typedef struct af_fwd_args {
+  af_spec_key key;
+  const void* q;       /* (B, H_q,  N_q,  D) */
+  const void* k;       /* (B, H_kv, N_kv, D) */
+  const void* v;       /* (B, H_kv, N_kv, D) */
+  void* o;             /* (B, H_q,  N_q,  D), dtype of q                   */
+  float* lse;          /* nullable: (B, H_q, N_q) fp32 log-sum-exp (ln)    */
+  const void* cos;     /* rope: (N_rope, D) table in q's dtype             */
+  const void* sin;
+  const float* alibi_slopes; /* ALiBi: (H_q) fp32                          */
+  const void* bias;    /* additive: (B, H_q, N_q, N_kv) in q's dtype       */
+  uint32_t* coverage;  /* nullable: (B, H_q, ceil(N_q/32), ceil(N_kv/64))
+                          visit counters, for mask-coverage tests          */
+  int64_t q_stride[4], k_stride[4], v_stride[4], o_stride[4];
+  int64_t lse_stride[3];
+  int64_t rope_stride[2]; /* (n, d) */
+  int64_t bias_stride[4];
+  int32_t batch, heads_q, heads_kv, seqlen_q, seqlen_kv, rope_len;
+  float scale;
+  int32_t window;      /* sliding window size (AF_MASK_SLIDING_WINDOW)     */
+} af_fwd_args;
+
+int af_fwd(const af_fwd_args* args, void* stream);
+
+/* Block-sparse forward.  Replaces attnfuse_blocksparse_fwd_kernel
+ * (reference: attnfuse/runtime/block_mask.py:205-271,
+ * attnfuse/compiler/codegen_blocksparse.py:34-171).  args->key.mask must be
+ * AF_MASK_BLOCK_SPARSE; the tile visited per listed block is whole (no
+ * element mask inside it, reference semantics). */
+int af_fwd_blocksparse(const af_fwd_args* args, const af_blockmask* bm,
+                       void* stream);
+
+/* Flash-decoding (one query row per head, split-K over the cache, then a
+ * log-sum-exp combine).  Replaces attnfuse_decode_split_kernel +
+ * attnfuse_decode_combine_kernel (reference:
+ * attnfuse/runtime/flash_decode.py:101-187,
+ * attnfuse/compiler/codegen_decode.py:46-211).  key.mask must be FULL and
+ * key.bias NONE or ALIBI, key.rope 0. */
+typedef struct af_decode_args {
+  af_spec_key key;
+  const void* q;  /* (B, H_q, 1, D)     */
+  const void* k;  /* (B, H_kv, N_kv, D) */
+  const void* v;
+  void* o;        /* (B, H_q, 1, D)     */
+  const float* alibi_slopes;
+  int64_t q_stride[4], k_stride[4], v_stride[4], o_stride[4];
+  int32_t batch, heads_q, heads_kv, seqlen_kv;
+  float scale;
+  int32_t num_splits; /* <= 0: library default (af_decode_num_splits) */
+} af_decode_args;
+
+int32_t af_decode_num_splits(int32_t batch, int32_t heads_q, int32_t heads_kv,
+                             int32_t seqlen_kv, int32_t head_dim);
+size_t af_decode_workspace_bytes(int32_t batch, int32_t heads_q,
+                                 int32_t head_dim, int32_t num_splits);
+int af_decode(const af_decode_args* args, void* workspace,
+              size_t workspace_bytes, void* stream);
+
+/* Backward (FA2 style: delta = rowsum(dO*O), then dK/dV, then dQ).
+ * Replaces attnfuse_bwd_{preproc,dkv,dq}_kernel and the block-sparse dkv/dq
+ * kernels (reference: attnfuse/runtime/backward.py:83-192,
+ * attnfuse/runtime/block_mask.py:274-363).  Supports softmax with FULL,
+ * CAUSAL, SLIDING_WINDOW and BLOCK_SPARSE masks, NONE/ALIBI bias and fused
+ * RoPE (the gradients are rotated back to the input space).  dK/dV of a
+ * key/value head are summed over its query-head group in-kernel. */
+typedef struct af_bwd_args {
+  af_spec_key key;
+  const void *q, *k, *v, *o, *dout;
+  const float* lse;  /* (B, H_q, N_q) fp32, from the forward */
+  void *dq, *dk, *dv;
+  const void* cos;
+  const void* sin;
+  const float* alibi_slopes;
+  int64_t q_stride[4], k_stride[4], v_stride[4], o_stride[4], do_stride[4];
+  int64_t dq_stride[4], dk_stride[4], dv_stride[4];
+  int64_t lse_stride[3];
+  int64_t rope_stride[2];
+  int32_t batch, heads_q, heads_kv, seqlen_q, seqlen_kv, rope_len;
+  float scale;
+  int32_t window;
+} af_bwd_args;
+
+size_t af_bwd_workspace_bytes(int32_t batch, int32_t heads_q,
+                              int32_t seqlen_q);
+int af_bwd(const af_bwd_args* args, const af_blockmask* bm /* nullable */,
+           void* workspace, size_t workspace_bytes, void* stream);
+
+/* 1 if an instantiation exists for the key (forward; decode and backward
+ * accept the subsets documented above), else 0. */
+int af_query(const af_spec_key* key);
+/* Forward tile shape used for the key: query rows per workgroup and keys per
+ * stage (the coverage counters are kept per 32 query rows x 64 keys). */
+int af_fwd_tile(const af_spec_key* key, int32_t* block_m, int32_t* block_n);
+
+const char* af_last_error(void);
+int af_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATTNFUSE_HIP_H */

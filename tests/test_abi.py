@@ -1,0 +1,121 @@
+"""The C-ABI library: it loads, exports every symbol the header declares,
+its structs have the layout the ctypes binding assumes, and its argument
+checks answer without touching a GPU."""
+import ctypes as C
+import re
+import subprocess
+import textwrap
+from pathlib import Path
+
+import pytest
+
+from attentionfuse_amd.runtime import _native as N
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "attnfuse_hip.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(af_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_reports_abi():
+    lib = N.lib()
+    assert lib.af_abi_version() == 1
+
+
+def test_every_declared_symbol_is_exported():
+    names = _declared_functions()
+    assert "af_fwd" in names and "af_decode" in names and "af_bwd" in names
+    lib = C.CDLL(str(N.library_path()))
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(N.SIGNATURES)
+
+
+def test_struct_layouts_match_header(tmp_path):
+    structs = {"af_spec_key": N.SpecKeyC, "af_blockmask": N.BlockMaskC,
+               "af_fwd_args": N.FwdArgsC, "af_decode_args": N.DecodeArgsC,
+               "af_bwd_args": N.BwdArgsC}
+    lines = []
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in py._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    src = tmp_path / "layout.c"
+    src.write_text(textwrap.dedent(f"""
+        #include <stdio.h>
+        #include <stddef.h>
+        #include "attnfuse_hip.h"
+        int main(void) {{ {' '.join(lines)} return 0; }}
+    """))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)],
+                   check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+    for line in out.splitlines():
+        cname, field, val = line.split()
+        py = structs[cname]
+        want = C.sizeof(py) if field == "size" else getattr(py, field).offset
+        assert int(val) == want, (cname, field)
+
+
+def test_query_and_tile():
+    lib = N.lib()
+    assert lib.af_query(N.SpecKeyC(0, 64, 1, 1, 0, 1)) == 1
+    assert lib.af_query(N.SpecKeyC(1, 128, 3, 0, 0, 0)) == 1
+    assert lib.af_query(N.SpecKeyC(2, 64, 0, 0, 0, 0)) == 0      # fp32
+    assert lib.af_query(N.SpecKeyC(0, 80, 0, 0, 0, 0)) == 0      # head_dim
+    bm, bn = C.c_int32(), C.c_int32()
+    assert lib.af_fwd_tile(N.SpecKeyC(0, 64, 1, 0, 0, 0), C.byref(bm), C.byref(bn)) == 0
+    assert (bm.value, bn.value) == (128, 64)
+
+
+def test_argument_errors_need_no_gpu():
+    lib = N.lib()
+    a = N.FwdArgsC()
+    a.key = N.SpecKeyC(0, 64, 1, 0, 0, 0)
+    assert lib.af_fwd(a, None) == N.AF_ERR_BAD_ARG
+    assert "NULL" in N.last_error()
+    assert lib.af_fwd(None, None) == N.AF_ERR_BAD_ARG
+    # misaligned / non-unit strides are refused before any launch
+    a.q = a.k = a.v = a.o = 16
+    for s in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
+        s[:] = (64 * 4 * 64, 64 * 64, 64, 2)
+    a.batch, a.heads_q, a.heads_kv, a.seqlen_q, a.seqlen_kv = 1, 4, 4, 64, 64
+    assert lib.af_fwd(a, None) == N.AF_ERR_BAD_ARG
+    assert "stride" in N.last_error()
+    for s in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
+        s[:] = (64 * 4 * 64, 64 * 64, 64, 1)
+    a.heads_kv = 3
+    assert lib.af_fwd(a, None) == N.AF_ERR_BAD_ARG
+    assert "multiple" in N.last_error()
+    a.heads_kv = 4
+    a.seqlen_kv = 32
+    assert lib.af_fwd(a, None) == N.AF_ERR_BAD_ARG        # causal needs Nq == Nkv
+    a.key = N.SpecKeyC(2, 64, 0, 0, 0, 0)
+    assert lib.af_fwd(a, None) == N.AF_ERR_UNSUPPORTED
+    with pytest.raises(NotImplementedError):
+        N.check(N.AF_ERR_UNSUPPORTED)
+    with pytest.raises(ValueError):
+        N.check(N.AF_ERR_BAD_ARG)
+
+
+def test_decode_split_and_workspace_arithmetic():
+    lib = N.lib()
+    s = lib.af_decode_num_splits(8, 32, 8, 32768, 128)
+    assert 1 <= s <= 256
+    assert lib.af_decode_num_splits(1, 1, 1, 300, 64) == 1
+    assert lib.af_decode_workspace_bytes(8, 32, 128, 16) == 16 * 8 * 32 * 130 * 4
+    a = N.DecodeArgsC()
+    a.key = N.SpecKeyC(1, 128, 0, 0, 0, 0)
+    a.q = a.k = a.v = a.o = 256
+    for st in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
+        st[:] = (8 * 128, 128, 128, 1)
+    a.batch, a.heads_q, a.heads_kv, a.seqlen_kv = 1, 8, 2, 1024
+    a.scale, a.num_splits = 0.1, 4
+    assert lib.af_decode(a, None, 0, None) == N.AF_ERR_WORKSPACE
+    a.key = N.SpecKeyC(1, 128, 1, 0, 0, 0)
+    assert lib.af_decode(a, None, 0, None) == N.AF_ERR_UNSUPPORTED

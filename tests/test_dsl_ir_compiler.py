@@ -1,0 +1,218 @@
+"""DSL, IR and compiler behaviour on the CPU (the reference's
+tests/test_dsl.py, test_ir.py, test_compiler.py and the CPU half of
+test_smoke.py), through the drop-in import name ``attnfuse``."""
+import math
+
+import pytest
+import torch
+
+import attnfuse as af
+from attnfuse.compiler.fusion import FusionError, fuse_score_softmax
+from attnfuse.compiler.lowering import kernel_constexprs, lower_to_tiled
+from attnfuse.compiler.tiling import choose_tile_config
+from attnfuse.ir.high_level import (BiasKind, Graph, MaskKind, MatMulPV,
+                                    NormKind, NormOp, ScoreKind, ScoreOp)
+from attnfuse.ir.printer import format_graph, format_tiled
+
+
+def _zeros(D=32, N=16, H=2):
+    z = torch.zeros(1, H, N, D)
+    return z, z.clone(), z.clone()
+
+
+def _trace(fn, D=64, H=4, N=16):
+    return fn(*_zeros(D, N, H), return_graph=True)
+
+
+def test_import_and_version():
+    assert af.__version__
+    import attentionfuse_amd
+    assert af.attention is attentionfuse_amd.attention
+
+
+def test_dense_graph_shape():
+    @af.attention
+    def fn(Q, K, V):
+        return af.softmax(af.scaled_dot_product(Q, K)) @ V
+    g = fn(*_zeros(), return_graph=True)
+    assert g.score().scale is None
+    assert g.collect_masks() == []
+    assert g.norm().kind == NormKind.SOFTMAX
+    assert g.q.head_dim == 32 and len(g.signature()) == 16
+
+
+def test_causal_alibi_graph():
+    @af.attention
+    def fn(Q, K, V):
+        s = af.scaled_dot_product(Q, K)
+        s = af.alibi(s, num_heads=2)
+        s = af.causal(s)
+        return af.softmax(s) @ V
+    g = fn(*_zeros(), return_graph=True)
+    assert [m.kind for m in g.collect_masks()] == [MaskKind.CAUSAL]
+    assert [b.kind for b in g.collect_biases()] == [BiasKind.ALIBI]
+
+
+def test_combinator_argument_checks():
+    with pytest.raises(ValueError):
+        @af.attention
+        def fn(Q, K, V):
+            return af.softmax(af.sliding_window(af.scaled_dot_product(Q, K), 0)) @ V
+        fn(*_zeros(), return_graph=True)
+    with pytest.raises(ValueError):
+        @af.attention
+        def fn2(Q, K, V):
+            return af.softmax(af.alibi(af.scaled_dot_product(Q, K), num_heads=0)) @ V
+        fn2(*_zeros(), return_graph=True)
+
+
+def test_missing_value_projection_message():
+    @af.attention
+    def fn(Q, K, V):
+        return af.softmax(af.scaled_dot_product(Q, K))
+    with pytest.raises(TypeError, match="value projection"):
+        fn(*_zeros(), return_graph=True)
+
+
+def test_probs_must_be_normalised():
+    @af.attention
+    def fn(Q, K, V):
+        return af.scaled_dot_product(Q, K) @ V
+    with pytest.raises(TypeError):
+        fn(*_zeros(), return_graph=True)
+
+
+def test_tracer_rejects_bad_shapes():
+    @af.attention
+    def fn(Q, K, V):
+        return af.softmax(af.scaled_dot_product(Q, K)) @ V
+    with pytest.raises(ValueError):
+        fn(torch.zeros(2, 16, 32), torch.zeros(2, 16, 32), torch.zeros(2, 16, 32),
+           return_graph=True)
+    with pytest.raises(ValueError):
+        fn(torch.zeros(1, 2, 16, 32), torch.zeros(1, 2, 16, 64),
+           torch.zeros(1, 2, 16, 64), return_graph=True)
+
+
+def test_signature_stable_and_discriminating():
+    def make(variant):
+        @af.attention
+        def fn(Q, K, V):
+            s = af.scaled_dot_product(Q, K)
+            if variant == "causal":
+                s = af.causal(s)
+            if variant == "rope":
+                s = af.causal(af.rope(Q, K))
+            return af.softmax(s) @ V
+        return fn(*_zeros(), return_graph=True).signature()
+    assert make("causal") == make("causal")
+    assert len({make("causal"), make("dense"), make("rope")}) == 3
+    # sizes do not enter the signature; dtype and head_dim do
+    @af.attention
+    def fn(Q, K, V):
+        return af.softmax(af.scaled_dot_product(Q, K)) @ V
+    a = fn(*_zeros(N=16), return_graph=True).signature()
+    assert a == af.attention(fn.graph_fn)(*_zeros(N=99, H=5), return_graph=True).signature()
+    z = torch.zeros(1, 2, 16, 32, dtype=torch.float16)
+    assert a != af.attention(fn.graph_fn)(z, z, z, return_graph=True).signature()
+
+
+def _g():
+    @af.attention
+    def fn(Q, K, V):
+        s = af.scaled_dot_product(Q, K)
+        s = af.alibi(s, num_heads=4)
+        s = af.causal(s)
+        return af.softmax(s) @ V
+    Q = torch.zeros(1, 4, 16, 64)
+    return fn(Q, Q.clone(), Q.clone(), return_graph=True)
+
+
+def test_printers():
+    s = format_graph(_g())
+    assert "MatMulPV" in s and "ScoreOp" in s
+    assert "BLOCK_M" in format_tiled(lower_to_tiled(_g()))
+
+
+def test_lowering_collapses_to_key():
+    k = lower_to_tiled(_g())
+    assert k.head_dim == 64
+    assert k.mask_kind is MaskKind.CAUSAL
+    assert k.bias_kind is BiasKind.ALIBI
+    assert k.norm_kind is NormKind.SOFTMAX
+    assert abs(k.score_scale - 1.0 / 8.0) < 1e-9
+    assert k.abi_tuple() == (2, 64, 1, 1, 0, 0)
+
+
+def test_lowering_folds_and_rejects_masks():
+    @af.attention
+    def sw_causal(Q, K, V):
+        return af.softmax(af.causal(af.sliding_window(af.scaled_dot_product(Q, K), 8))) @ V
+    k = lower_to_tiled(_trace(sw_causal))
+    assert k.mask_kind is MaskKind.SLIDING_WINDOW and k.mask_window == 8
+
+    @af.attention
+    def two_bias(Q, K, V):
+        s = af.additive_bias(af.alibi(af.scaled_dot_product(Q, K), 4))
+        return af.softmax(s) @ V
+    with pytest.raises(NotImplementedError):
+        lower_to_tiled(_trace(two_bias))
+
+    @af.attention
+    def bs_causal(Q, K, V):
+        return af.softmax(af.causal(af.block_sparse(af.scaled_dot_product(Q, K)))) @ V
+    with pytest.raises(NotImplementedError):
+        lower_to_tiled(_trace(bs_causal))
+
+
+def test_custom_scale_and_rope_flag():
+    @af.attention
+    def fn(Q, K, V):
+        return af.relu_attention(af.rope(Q, K, scale=0.5)) @ V
+    k = lower_to_tiled(_trace(fn))
+    assert k.score_scale == 0.5 and k.rope_kind == 1 and k.norm_kind is NormKind.RELU
+
+
+def test_fusion_checks():
+    @af.attention
+    def fn(Q, K, V):
+        return af.softmax(af.causal(af.scaled_dot_product(Q, K))) @ V
+    g = _trace(fn)
+    fuse_score_softmax(g)
+    bad = Graph(q=g.q, k=g.k, v=g.v,
+                root=MatMulPV(probs=NormOp(kind=NormKind.SOFTMAX, scores=g.q), v=g.v))
+    with pytest.raises(FusionError):
+        fuse_score_softmax(bad)
+
+
+def test_tile_config_for_each_head_dim():
+    for D in (32, 64, 96, 128, 256):
+        @af.attention
+        def fn(Q, K, V):
+            return af.softmax(af.scaled_dot_product(Q, K)) @ V
+        cfg = choose_tile_config(_trace(fn, D=D))
+        assert cfg.BLOCK_M >= 32 and cfg.BLOCK_N >= 16
+        assert cfg.BLOCK_M == 32 * cfg.waves
+
+
+def test_constexprs_change_with_variant():
+    @af.attention
+    def dense(Q, K, V):
+        return af.softmax(af.scaled_dot_product(Q, K)) @ V
+
+    @af.attention
+    def causal(Q, K, V):
+        return af.softmax(af.causal(af.scaled_dot_product(Q, K))) @ V
+    cd = kernel_constexprs(lower_to_tiled(_trace(dense)))
+    cc = kernel_constexprs(lower_to_tiled(_trace(causal)))
+    assert cd["MASK_KIND"] != cc["MASK_KIND"]
+
+
+def test_debug_printing(capsys, monkeypatch):
+    monkeypatch.setenv("ATTNFUSE_DEBUG", "1")
+
+    @af.attention
+    def fn(Q, K, V):
+        return af.softmax(af.scaled_dot_product(Q, K)) @ V
+    fn(*_zeros(), return_graph=True)
+    assert "traced graph" in capsys.readouterr().out

@@ -1,0 +1,215 @@
+"""Forward kernel parity on the GPU against the fp32 CPU oracle.
+
+Tolerances (max-abs, against an fp32 oracle fed the same 16-bit input
+values): fp16 2e-3, bf16 1.6e-2.  Coverage counters must equal the expected
+tile sets exactly.  Mirrors the reference's tests/test_correctness.py,
+test_gqa.py and test_cross_attention.py cases at the tighter tolerances.
+"""
+import math
+
+import pytest
+import torch
+
+import attnfuse as af
+import oracle as O
+from attnfuse.rope_utils import build_rope_cache
+from attnfuse.runtime.dispatch import _alibi_slopes, run_attention
+
+pytestmark = pytest.mark.gpu
+TOL = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
+LSE_TOL = {torch.float16: 5e-3, torch.bfloat16: 3e-2}
+
+
+def make(B, Hq, Hkv, Nq, Nkv, D, dtype, seed=0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    Q = torch.randn(B, Hq, Nq, D, generator=g, device="cuda", dtype=dtype)
+    K = torch.randn(B, Hkv, Nkv, D, generator=g, device="cuda", dtype=dtype)
+    V = torch.randn(B, Hkv, Nkv, D, generator=g, device="cuda", dtype=dtype)
+    return Q, K, V
+
+
+def variant(name, H, window=32, scale=None):
+    if name == "dense":
+        return lambda Q, K, V: af.softmax(af.scaled_dot_product(Q, K, scale)) @ V
+    if name == "causal":
+        return lambda Q, K, V: af.softmax(af.causal(af.scaled_dot_product(Q, K, scale))) @ V
+    if name == "sw":
+        return lambda Q, K, V: af.softmax(af.sliding_window(af.scaled_dot_product(Q, K), window)) @ V
+    if name == "sw_causal":
+        return lambda Q, K, V: af.softmax(af.causal(af.sliding_window(af.scaled_dot_product(Q, K), window))) @ V
+    if name == "alibi":
+        return lambda Q, K, V: af.softmax(af.alibi(af.scaled_dot_product(Q, K), H)) @ V
+    if name == "causal_alibi":
+        return lambda Q, K, V: af.softmax(af.causal(af.alibi(af.scaled_dot_product(Q, K), H))) @ V
+    if name == "additive":
+        return lambda Q, K, V: af.softmax(af.additive_bias(af.scaled_dot_product(Q, K))) @ V
+    if name == "relu":
+        return lambda Q, K, V: af.relu_attention(af.causal(af.scaled_dot_product(Q, K))) @ V
+    if name == "rope_causal":
+        return lambda Q, K, V: af.softmax(af.causal(af.rope(Q, K))) @ V
+    if name == "rope_causal_alibi":
+        return lambda Q, K, V: af.softmax(af.causal(af.alibi(af.rope(Q, K), H))) @ V
+    if name == "rope_dense":
+        return lambda Q, K, V: af.softmax(af.rope(Q, K, scale)) @ V
+    raise KeyError(name)
+
+
+def oracle_kwargs(name, H, Q, window=32, scale=None, bias=None, rope=None):
+    kw = {"scale": scale}
+    if "causal" in name:
+        kw["causal"] = True
+    if name.startswith("sw"):
+        kw["window"] = window
+    if "alibi" in name:
+        kw["alibi_slopes"] = _alibi_slopes(H, "cpu", str(Q.dtype)).float()
+    if name == "additive":
+        kw["bias"] = bias
+    if name == "relu":
+        kw["norm"] = "relu"
+    if name.startswith("rope"):
+        kw["rope"] = rope
+    return kw
+
+
+def run_case(name, B, Hq, Hkv, N, D, dtype, Nkv=None, scale=None, seed=0):
+    Nkv = N if Nkv is None else Nkv
+    Q, K, V = make(B, Hq, Hkv, N, Nkv, D, dtype, seed)
+    fn = af.attention(variant(name, Hq, scale=scale))
+    extra, rope, bias = {}, None, None
+    if name.startswith("rope"):
+        cos, sin = build_rope_cache(max(N, Nkv), D, device="cuda", dtype=dtype)
+        extra = {"cos": cos, "sin": sin}
+        rope = (cos[0, 0].cpu(), sin[0, 0].cpu())
+    if name == "additive":
+        g = torch.Generator(device="cuda").manual_seed(seed + 1)
+        bias = torch.randn(B, Hq, N, Nkv, generator=g, device="cuda", dtype=dtype)
+        extra = {"bias": bias}
+    out = fn(Q, K, V, **extra)
+    torch.cuda.synchronize()
+    want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(),
+                             **oracle_kwargs(name, Hq, Q, scale=scale,
+                                             bias=None if bias is None else bias.cpu(),
+                                             rope=rope))
+    err = (out.float().cpu() - want).abs().max().item()
+    return err
+
+
+VARIANTS = ["dense", "causal", "sw", "sw_causal", "alibi", "causal_alibi",
+            "additive", "relu", "rope_causal", "rope_causal_alibi"]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("name", VARIANTS)
+def test_variants_d64(name, dtype):
+    print(f"[fwd] {name} {dtype} B2 H4 N256 D64", flush=True)
+    err = run_case(name, 2, 4, 4, 256, 64, dtype)
+    assert err <= TOL[dtype], f"{name}: max|err|={err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("D", [32, 128])
+@pytest.mark.parametrize("name", ["dense", "causal", "rope_causal_alibi", "sw"])
+def test_head_dims(name, D, dtype):
+    print(f"[fwd] {name} {dtype} D{D}", flush=True)
+    err = run_case(name, 1, 4, 4, 192, D, dtype)
+    assert err <= TOL[dtype], f"{name} D={D}: max|err|={err:.3e}"
+
+
+@pytest.mark.parametrize("N", [1, 17, 64, 200, 333])
+@pytest.mark.parametrize("name", ["causal", "rope_causal", "sw", "dense", "additive"])
+def test_ragged_lengths(name, N):
+    print(f"[fwd] ragged {name} N{N}", flush=True)
+    err = run_case(name, 2, 2, 2, N, 64, torch.float16, seed=N)
+    assert err <= TOL[torch.float16], f"{name} N={N}: max|err|={err:.3e}"
+
+
+@pytest.mark.parametrize("heads", [(8, 8), (8, 2), (8, 1), (12, 4), (12, 1), (32, 8)])
+@pytest.mark.parametrize("name", ["dense", "causal", "sw", "causal_alibi", "rope_causal"])
+def test_gqa(name, heads):
+    Hq, Hkv = heads
+    print(f"[fwd] gqa {name} {Hq}/{Hkv}", flush=True)
+    err = run_case(name, 2, Hq, Hkv, 256, 64, torch.float16)
+    assert err <= TOL[torch.float16], f"{name} {heads}: max|err|={err:.3e}"
+
+
+@pytest.mark.parametrize("shape", [(64, 300), (100, 77), (1, 100), (256, 4096)])
+def test_cross_attention_dense(shape):
+    Nq, Nkv = shape
+    print(f"[fwd] cross {shape}", flush=True)
+    err = run_case("dense", 1, 4, 2, Nq, 64, torch.bfloat16, Nkv=Nkv)
+    assert err <= TOL[torch.bfloat16]
+
+
+def test_cross_attention_rejects_masks():
+    Q, K, V = make(1, 2, 2, 64, 128, 64, torch.float16)
+    with pytest.raises(ValueError, match="cross-attention"):
+        af.attention(variant("causal", 2))(Q, K, V)
+
+
+def test_custom_scale():
+    err = run_case("dense", 1, 2, 2, 128, 64, torch.float16, scale=0.05)
+    assert err <= TOL[torch.float16]
+    err = run_case("causal", 1, 2, 2, 128, 64, torch.float16, scale=0.3)
+    assert err <= TOL[torch.float16]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("name", ["causal", "rope_causal_alibi", "sw", "dense"])
+def test_saved_lse(name, dtype):
+    B, H, N, D = 2, 4, 200, 64
+    Q, K, V = make(B, H, H, N, N, D, dtype)
+    g = af.attention(variant(name, H))(Q, K, V, return_graph=True)
+    extra, rope = {}, None
+    if name.startswith("rope"):
+        cos, sin = build_rope_cache(N, D, device="cuda", dtype=dtype)
+        extra = {"cos": cos, "sin": sin}
+        rope = (cos[0, 0].cpu(), sin[0, 0].cpu())
+    L = torch.empty(B, H, N, dtype=torch.float32, device="cuda")
+    run_attention(g, Q, K, V, save_lse=L, **extra)
+    torch.cuda.synchronize()
+    _, Lw = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(), return_lse=True,
+                              **oracle_kwargs(name, H, Q, rope=rope))
+    assert (L.cpu() - Lw).abs().max().item() <= LSE_TOL[dtype]
+
+
+def test_strided_inputs_match_contiguous():
+    B, N, H, D = 2, 130, 4, 64
+    g = torch.Generator(device="cuda").manual_seed(3)
+    base = torch.randn(3, B, N, H, D, generator=g, device="cuda", dtype=torch.float16)
+    Qs, Ks, Vs = (base[i].transpose(1, 2) for i in range(3))   # (B,H,N,D) views
+    fn = af.attention(variant("causal", H))
+    a = fn(Qs, Ks, Vs)
+    b = fn(Qs.contiguous(), Ks.contiguous(), Vs.contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_deterministic():
+    Q, K, V = make(2, 4, 4, 300, 300, 64, torch.bfloat16)
+    fn = af.attention(variant("rope_causal_alibi", 4))
+    cos, sin = build_rope_cache(300, 64, device="cuda", dtype=torch.bfloat16)
+    a = fn(Q, K, V, cos=cos, sin=sin)
+    b = fn(Q, K, V, cos=cos, sin=sin)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("mask,N", [("causal", 256), ("causal", 333), ("sw", 300), ("full", 200)])
+def test_tile_coverage_exact(mask, N):
+    B, H, D, W = 2, 3, 64, 40
+    Q, K, V = make(B, H, H, N, N, D, torch.float16)
+    name = {"causal": "causal", "sw": "sw", "full": "dense"}[mask]
+    g = af.attention(variant(name, H, window=W))(Q, K, V, return_graph=True)
+    cov = torch.zeros(B, H, -(-N // 32), -(-N // 64), dtype=torch.int32, device="cuda")
+    run_attention(g, Q, K, V, coverage=cov)
+    torch.cuda.synchronize()
+    want = O.expected_coverage(N, N, mask={"sw": "sliding_window"}.get(mask, mask), window=W)
+    assert torch.equal(cov.cpu(), want.expand(B, H, *want.shape))
+
+
+def test_smoke_dense_matches_reference_test():
+    """Reference tests/test_smoke.py::test_dispatch_dense_gpu."""
+    fn = af.attention(variant("dense", 2))
+    Q = torch.randn(1, 2, 64, 32, device="cuda", dtype=torch.float16)
+    out = fn(Q, torch.randn_like(Q), torch.randn_like(Q))
+    assert out.shape == Q.shape and torch.isfinite(out).all()
