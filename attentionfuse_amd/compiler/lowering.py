@@ -4,8 +4,11 @@ Same folding rules as the reference lowering
 (reference: attnfuse/compiler/lowering.py:20-85):
 
 * the score scale defaults to 1/sqrt(head_dim);
-* causal + sliding_window folds to sliding_window (the window is the stricter
-  mask for every key after the query); any other pair of masks is rejected;
+* causal + sliding_window lowers to one causal-window mask (key j visible to
+  query i iff i - W < j <= i); any other pair of masks is rejected.  The
+  reference folds this pair to the plain (two-sided) window
+  (attnfuse/compiler/lowering.py:32-46), which lets each query see W-1 future
+  keys -- a different function from the graph the user wrote;
 * at most one bias op;
 * ``rope_kind`` is 1 when the score op carries fused RoPE.
 """
@@ -32,7 +35,7 @@ def lower_to_key(graph: Graph) -> SpecKey:
     if len(masks) > 1:
         if kinds == {MaskKind.CAUSAL, MaskKind.SLIDING_WINDOW}:
             sw = next(m for m in masks if m.kind is MaskKind.SLIDING_WINDOW)
-            mask_kind, window = MaskKind.SLIDING_WINDOW, sw.window
+            mask_kind, window = MaskKind.CAUSAL_SLIDING_WINDOW, sw.window
         else:
             raise NotImplementedError(
                 f"mask combination {sorted(k.value for k in kinds)} is not "

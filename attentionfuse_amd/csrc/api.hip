@@ -11,6 +11,7 @@
 #include "bwd_launch.hpp"
 #include "launch.hpp"
 #include "launch_decode.hpp"
+#include "validate.hpp"
 
 namespace af {
 
@@ -35,25 +36,12 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-// (B, H, N, D) tensor with unit D-stride, 16-byte aligned rows.
-int check_bhnd(const char* name, const void* ptr, const int64_t* st) {
-  if (ptr == nullptr) return fail(AF_ERR_BAD_ARG, "%s is NULL", name);
-  if (st[3] != 1) return fail(AF_ERR_BAD_ARG, "%s: head-dim stride must be 1 (got %lld)", name, (long long)st[3]);
-  if (!aligned16(ptr)) return fail(AF_ERR_BAD_ARG, "%s: base pointer must be 16-byte aligned", name);
-  for (int i = 0; i < 3; ++i)
-    if (st[i] % 8 != 0)
-      return fail(AF_ERR_BAD_ARG, "%s: stride[%d]=%lld is not a multiple of 8 elements", name, i, (long long)st[i]);
-  return AF_OK;
-}
-
 int check_key(const af_spec_key& k, bool allow_bs) {
   if (k.dtype != AF_F16 && k.dtype != AF_BF16)
     return fail(AF_ERR_UNSUPPORTED, "dtype %d: the gfx950 kernels take fp16 or bf16", k.dtype);
   if (k.head_dim != 32 && k.head_dim != 64 && k.head_dim != 128)
     return fail(AF_ERR_UNSUPPORTED, "head_dim %d: instantiated for 32, 64 and 128", k.head_dim);
-  if (k.mask < 0 || k.mask > 3 || (!allow_bs && k.mask == AF_MASK_BLOCK_SPARSE))
+  if (k.mask < 0 || k.mask > 4 || (!allow_bs && k.mask == AF_MASK_BLOCK_SPARSE))
     return fail(AF_ERR_UNSUPPORTED, "mask kind %d not valid here", k.mask);
   if (k.bias < 0 || k.bias > 2) return fail(AF_ERR_UNSUPPORTED, "bias kind %d", k.bias);
   if (k.norm < 0 || k.norm > 1) return fail(AF_ERR_UNSUPPORTED, "norm kind %d", k.norm);
@@ -75,10 +63,11 @@ int check_fwd_common(const af_fwd_args* a) {
     return fail(AF_ERR_BAD_ARG, "query heads (%d) must be a multiple of key/value heads (%d)", a->heads_q,
                 a->heads_kv);
   const af_spec_key& k = a->key;
-  if ((k.mask == AF_MASK_CAUSAL || k.mask == AF_MASK_SLIDING_WINDOW) && a->seqlen_q != a->seqlen_kv)
+  if ((k.mask == AF_MASK_CAUSAL || k.mask == AF_MASK_SLIDING_WINDOW ||
+       k.mask == AF_MASK_CAUSAL_SLIDING_WINDOW) && a->seqlen_q != a->seqlen_kv)
     return fail(AF_ERR_BAD_ARG, "causal / sliding-window masks need seqlen_q == seqlen_kv (%d vs %d)",
                 a->seqlen_q, a->seqlen_kv);
-  if (k.mask == AF_MASK_SLIDING_WINDOW && a->window <= 0)
+  if ((k.mask == AF_MASK_SLIDING_WINDOW || k.mask == AF_MASK_CAUSAL_SLIDING_WINDOW) && a->window <= 0)
     return fail(AF_ERR_BAD_ARG, "sliding window size must be positive");
   if (k.rope) {
     if (a->cos == nullptr || a->sin == nullptr) return fail(AF_ERR_BAD_ARG, "rope needs cos and sin tables");
@@ -293,7 +282,7 @@ int af_decode(const af_decode_args* a, void* workspace, size_t workspace_bytes, 
   p.split_len = split_len;
   p.scale = a->scale;
   const dim3 gs((unsigned)S, (unsigned)(a->batch * a->heads_kv * p.nqc));
-  const dim3 gc((unsigned)((a->batch * a->heads_q + 3) / 4));
+  const dim3 gc((unsigned)(a->batch * a->heads_q));
   if (launch_decode(p, a->key.dtype, D, a->key.bias, gs, gc, static_cast<hipStream_t>(stream)) != 0)
     return fail(AF_ERR_UNSUPPORTED, "no decode instantiation for this key");
   const hipError_t e = hipGetLastError();

@@ -37,7 +37,8 @@ UNITS = [
     ("decode", "decode_inst.hip", []),
     ("bwd", "bwd.hip", []),
 ] + [
-    (f"fwd_{dt}_d{d}", "fwd_inst.hip", [f"-DAF_DT={code}", f"-DAF_D={d}"])
+    (f"{kind}_{dt}_d{d}", f"{kind}_inst.hip", [f"-DAF_DT={code}", f"-DAF_D={d}"])
+    for kind in ("fwd", "bwd")
     for dt, code in (("f16", 0), ("bf16", 1)) for d in (32, 64, 128)
 ]
 

@@ -1,14 +1,159 @@
-// Backward launch (placeholder until the backward kernels land).
+// Backward entry point: validation, grid shapes and the three launches
+// (delta, dK/dV, dQ) on the caller's stream.
+#include <string.h>
+
+#include <algorithm>
+
 #include "bwd_launch.hpp"
 #include "launch.hpp"
+#include "validate.hpp"
 
 namespace af {
+
 size_t bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q) {
   if (batch <= 0 || heads_q <= 0 || seqlen_q < 0) return 0;
   return (size_t)batch * heads_q * seqlen_q * sizeof(float);
 }
-int run_bwd(const af_bwd_args*, const af_blockmask*, void*, size_t, hipStream_t) {
-  set_error("backward kernels are not built yet");
-  return AF_ERR_UNSUPPORTED;
+
+static int bad(int code, const char* msg) {
+  set_error("%s", msg);
+  return code;
 }
+
+int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_t workspace_bytes,
+            hipStream_t stream) {
+  if (a == nullptr) return bad(AF_ERR_BAD_ARG, "args is NULL");
+  const af_spec_key& k = a->key;
+  if (k.dtype != AF_F16 && k.dtype != AF_BF16) return bad(AF_ERR_UNSUPPORTED, "backward takes fp16 or bf16");
+  if (!head_dim_supported(k.head_dim)) return bad(AF_ERR_UNSUPPORTED, "backward head_dim must be 32, 64 or 128");
+  if (k.mask < 0 || k.mask > 4) return bad(AF_ERR_UNSUPPORTED, "unknown mask kind");
+  if (k.bias != AF_BIAS_NONE && k.bias != AF_BIAS_ALIBI)
+    return bad(AF_ERR_UNSUPPORTED, "backward supports no bias or ALiBi");
+  if (k.norm != AF_NORM_SOFTMAX) return bad(AF_ERR_UNSUPPORTED, "backward supports softmax normalisation only");
+  if (k.rope != 0 && k.rope != 1) return bad(AF_ERR_UNSUPPORTED, "unknown rope kind");
+  int rc;
+  const char* names[8] = {"q", "k", "v", "o", "dout", "dq", "dk", "dv"};
+  const void* ptrs[8] = {a->q, a->k, a->v, a->o, a->dout, a->dq, a->dk, a->dv};
+  const int64_t* strides[8] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride,
+                               a->do_stride, a->dq_stride, a->dk_stride, a->dv_stride};
+  for (int i = 0; i < 8; ++i)
+    if ((rc = check_bhnd(names[i], ptrs[i], strides[i]))) return rc;
+  if (a->lse == nullptr) return bad(AF_ERR_BAD_ARG, "lse is NULL");
+  if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seqlen_q < 0 || a->seqlen_kv < 0 ||
+      a->heads_q % a->heads_kv != 0)
+    return bad(AF_ERR_BAD_ARG, "bad sizes (or query heads not a multiple of key/value heads)");
+  if ((k.mask == AF_MASK_CAUSAL || k.mask == AF_MASK_SLIDING_WINDOW || k.mask == AF_MASK_CAUSAL_SLIDING_WINDOW) &&
+      a->seqlen_q != a->seqlen_kv)
+    return bad(AF_ERR_BAD_ARG, "causal / sliding-window masks need seqlen_q == seqlen_kv");
+  if ((k.mask == AF_MASK_SLIDING_WINDOW || k.mask == AF_MASK_CAUSAL_SLIDING_WINDOW) && a->window <= 0)
+    return bad(AF_ERR_BAD_ARG, "sliding window size must be positive");
+  if (k.rope) {
+    if (a->cos == nullptr || a->sin == nullptr) return bad(AF_ERR_BAD_ARG, "rope needs cos and sin tables");
+    if (a->rope_stride[1] != 1 || a->rope_stride[0] % 8 != 0 || !aligned16(a->cos) || !aligned16(a->sin))
+      return bad(AF_ERR_BAD_ARG, "rope tables need unit d-stride, 16-byte aligned rows");
+    if (a->rope_len < std::max(a->seqlen_q, a->seqlen_kv)) return bad(AF_ERR_BAD_ARG, "rope tables too short");
+  }
+  if (k.bias == AF_BIAS_ALIBI && a->alibi_slopes == nullptr) return bad(AF_ERR_BAD_ARG, "ALiBi needs slopes");
+  const size_t need = bwd_workspace_bytes(a->batch, a->heads_q, a->seqlen_q);
+  if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+    return bad(AF_ERR_WORKSPACE, "backward workspace too small (af_bwd_workspace_bytes)");
+
+  BwdParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.o = static_cast<const uint16_t*>(a->o);
+  p.dout = static_cast<const uint16_t*>(a->dout);
+  p.lse = a->lse;
+  p.delta = static_cast<float*>(workspace);
+  p.dq = static_cast<uint16_t*>(a->dq);
+  p.dk = static_cast<uint16_t*>(a->dk);
+  p.dv = static_cast<uint16_t*>(a->dv);
+  p.cos = static_cast<const uint16_t*>(a->cos);
+  p.sin = static_cast<const uint16_t*>(a->sin);
+  p.slopes = a->alibi_slopes;
+  for (int i = 0; i < 4; ++i) {
+    p.qs[i] = a->q_stride[i];
+    p.ks[i] = a->k_stride[i];
+    p.vs[i] = a->v_stride[i];
+    p.os[i] = a->o_stride[i];
+    p.dos[i] = a->do_stride[i];
+    p.dqs[i] = a->dq_stride[i];
+    p.dks[i] = a->dk_stride[i];
+    p.dvs[i] = a->dv_stride[i];
+  }
+  for (int i = 0; i < 3; ++i) p.ls[i] = a->lse_stride[i];
+  p.rs[0] = a->rope_stride[0];
+  p.rs[1] = a->rope_stride[1];
+  p.B = a->batch;
+  p.Hq = a->heads_q;
+  p.Hkv = a->heads_kv;
+  p.Nq = a->seqlen_q;
+  p.Nkv = a->seqlen_kv;
+  p.G = a->heads_q / a->heads_kv;
+  p.window = a->window;
+  p.scale = a->scale;
+
+  BwdGrids g;
+  g.waves_kv = 4;
+  g.waves_q = 4;
+  if (k.mask == AF_MASK_BLOCK_SPARSE) {
+    if (bm == nullptr || bm->full_kv_num == nullptr || bm->full_kv_idx == nullptr || bm->kv_num_blocks == nullptr ||
+        bm->kv_indices == nullptr || bm->q_num_blocks == nullptr || bm->q_indices == nullptr)
+      return bad(AF_ERR_BAD_ARG, "block-sparse backward needs the Q-major and K-major block lists");
+    if ((bm->block_m != 64 && bm->block_m != 128) || (bm->block_n != 64 && bm->block_n != 128))
+      return bad(AF_ERR_UNSUPPORTED, "block-sparse backward supports 64 or 128 blocks");
+    if (bm->n_q_blocks != (a->seqlen_q + bm->block_m - 1) / bm->block_m ||
+        bm->n_kv_blocks != (a->seqlen_kv + bm->block_n - 1) / bm->block_n)
+      return bad(AF_ERR_BAD_ARG, "block mask grid does not match the sequence lengths");
+    g.waves_kv = bm->block_n / 32;
+    g.waves_q = bm->block_m / 32;
+    p.bs_full_num = bm->full_kv_num;
+    p.bs_full_idx = bm->full_kv_idx;
+    p.bs_part_num = bm->kv_num_blocks;
+    p.bs_part_idx = bm->kv_indices;
+    p.bs_q_num = bm->q_num_blocks;
+    p.bs_q_idx = bm->q_indices;
+    p.bs_full_rs = bm->full_kv_stride;
+    p.bs_part_rs = bm->kv_stride;
+    p.bs_q_rs = bm->q_stride;
+    p.bs_block_m = bm->block_m;
+    p.bs_block_n = bm->block_n;
+  }
+  if (a->seqlen_q == 0 && a->seqlen_kv == 0) return AF_OK;
+  const int BK = 32 * g.waves_kv, BMq = 32 * g.waves_q;
+  p.n_kblocks = (a->seqlen_kv + BK - 1) / BK;
+  p.n_qblocks = (a->seqlen_q + BMq - 1) / BMq;
+  const int64_t rows = (int64_t)a->batch * a->heads_q * a->seqlen_q;
+  const int rpb = 256 / (k.head_dim / 8);
+  g.delta = (unsigned)std::max<int64_t>(1, (rows + rpb - 1) / rpb);
+  g.dkv = (unsigned)std::max(1, p.n_kblocks * a->batch * a->heads_kv);
+  g.dq = (unsigned)std::max(1, p.n_qblocks * a->batch * a->heads_q);
+
+  const bool f16 = k.dtype == AF_F16;
+  int r = -1;
+  switch (k.head_dim) {
+    case 32:
+      r = f16 ? launch_bwd_f16_d32(p, k.mask, k.bias, k.rope, g, stream)
+              : launch_bwd_bf16_d32(p, k.mask, k.bias, k.rope, g, stream);
+      break;
+    case 64:
+      r = f16 ? launch_bwd_f16_d64(p, k.mask, k.bias, k.rope, g, stream)
+              : launch_bwd_bf16_d64(p, k.mask, k.bias, k.rope, g, stream);
+      break;
+    case 128:
+      r = f16 ? launch_bwd_f16_d128(p, k.mask, k.bias, k.rope, g, stream)
+              : launch_bwd_bf16_d128(p, k.mask, k.bias, k.rope, g, stream);
+      break;
+  }
+  if (r != 0) return bad(AF_ERR_UNSUPPORTED, "no backward instantiation for this key");
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("backward launch failed: %s", hipGetErrorString(e));
+    return AF_ERR_LAUNCH;
+  }
+  return AF_OK;
+}
+
 }  // namespace af

@@ -223,37 +223,44 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeParams p)
   }
 }
 
-// Combine: one wave per (batch, query head); lanes own output dims.
+// Combine: one 256-thread workgroup per (batch, query head).  Thread t owns
+// output dim t % D and the splits s = t / D (mod 256 / D); the partial sums
+// of the split groups meet in LDS.  All loads of a thread are independent,
+// so the kernel is bound by the (L2-resident) workspace reads, not latency.
 template <class E, int D>
 __global__ void __launch_bounds__(256) decode_combine_kernel(const DecodeParams p) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);   // b * Hq + hq
-  if (row >= p.B * p.Hq) return;
+  constexpr int NG = 256 / D;
+  __shared__ float red_acc[NG][D];
+  __shared__ float red_l[NG];
+  const int t = threadIdx.x;
+  const int d = t % D, grp = t / D;
+  const int row = blockIdx.x;                 // b * Hq + hq
   const int b = row / p.Hq, hq = row - b * p.Hq;
-  const int64_t S = p.nsplit;
+  const int S = p.nsplit;
   const int64_t plane = (int64_t)p.B * p.Hq;
   float mstar = -INFINITY;
   for (int s = 0; s < S; ++s) mstar = fmaxf(mstar, p.ws_ml[2 * (s * plane + row)]);
   const float mu = (mstar == -INFINITY) ? 0.f : mstar;
-  float lsum = 0.f;
-  constexpr int PER = (D + 63) / 64;
-  float acc[PER] = {};
-  for (int s = 0; s < S; ++s) {
+  float acc = 0.f, lsum = 0.f;
+#pragma unroll 4
+  for (int s = grp; s < S; s += NG) {
     const int64_t r = s * plane + row;
     const float f = __builtin_amdgcn_exp2f(p.ws_ml[2 * r] - mu);
     lsum += f * p.ws_ml[2 * r + 1];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int d = lane + 64 * i;
-      if (d < D) acc[i] += f * p.ws_acc[r * D + d];
-    }
+    acc += f * p.ws_acc[r * D + d];
   }
-  const float inv = (lsum == 0.f) ? 1.f : 1.f / lsum;
-  uint16_t* orow = p.o + b * p.os[0] + hq * p.os[1];
+  red_acc[grp][d] = acc;
+  if (d == 0) red_l[grp] = lsum;
+  __syncthreads();
+  if (grp == 0) {
+    float a = 0.f, l = 0.f;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int d = lane + 64 * i;
-    if (d < D) orow[d] = E::one(acc[i] * inv);
+    for (int g2 = 0; g2 < NG; ++g2) {
+      a += red_acc[g2][d];
+      l += red_l[g2];
+    }
+    const float inv = (l == 0.f) ? 1.f : 1.f / l;
+    p.o[b * p.os[0] + hq * p.os[1] + d] = E::one(a * inv);
   }
 }
 

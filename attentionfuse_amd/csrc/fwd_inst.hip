@@ -79,6 +79,7 @@ int AF_FN(AF_DT_NAME, AF_D)(const FwdParams& p, int mask, int bias, int norm,
     case MASK_CAUSAL: return pick_bias<MASK_CAUSAL>(p, bias, norm, rope, waves, grid, s);
     case MASK_SW: return pick_bias<MASK_SW>(p, bias, norm, rope, waves, grid, s);
     case MASK_BS: return pick_bias<MASK_BS>(p, bias, norm, rope, waves, grid, s);
+    case MASK_CSW: return pick_bias<MASK_CSW>(p, bias, norm, rope, waves, grid, s);
     default: return -1;
   }
 }

@@ -27,7 +27,7 @@
 
 namespace af {
 
-enum { MASK_FULL = 0, MASK_CAUSAL = 1, MASK_SW = 2, MASK_BS = 3 };
+enum { MASK_FULL = 0, MASK_CAUSAL = 1, MASK_SW = 2, MASK_BS = 3, MASK_CSW = 4 };
 enum { BIAS_NONE = 0, BIAS_ALIBI = 1, BIAS_ADD = 2 };
 enum { NORM_SOFTMAX = 0, NORM_RELU = 1 };
 
@@ -128,6 +128,9 @@ __global__ void __launch_bounds__(WAVES * 64)
   } else if constexpr (MASK == MASK_SW) {
     n_lo = max(m0 - p.window + 1, 0) & ~(BN - 1);
     n_hi = min(m0 + BM - 1 + p.window, p.Nkv);
+  } else if constexpr (MASK == MASK_CSW) {
+    n_lo = max(m0 - p.window + 1, 0) & ~(BN - 1);
+    n_hi = min(m0 + BM, p.Nkv);
   }
   if constexpr (MASK == MASK_BS) {
     bs_sub = p.bs_block_n / BN;
@@ -243,6 +246,8 @@ __global__ void __launch_bounds__(WAVES * 64)
     if constexpr (MASK == MASK_CAUSAL) active = active && n0 <= q0w + 31;
     if constexpr (MASK == MASK_SW)
       active = active && n0 + BN - 1 > q0w - p.window && n0 < q0w + 31 + p.window;
+    if constexpr (MASK == MASK_CSW)
+      active = active && n0 + BN - 1 > q0w - p.window && n0 <= q0w + 31;
 
     if (active) {
       if (p.coverage != nullptr && lane == 0) {
@@ -264,6 +269,8 @@ __global__ void __launch_bounds__(WAVES * 64)
       if constexpr (MASK == MASK_CAUSAL) need_mask = need_mask || n0 + BN - 1 > q0w;
       if constexpr (MASK == MASK_SW)
         need_mask = need_mask || (q0w + 31 - n0 >= p.window) || (n0 + BN - 1 - q0w >= p.window);
+      if constexpr (MASK == MASK_CSW)
+        need_mask = need_mask || (q0w + 31 - n0 >= p.window) || n0 + BN - 1 > q0w;
 
       // scores -> log2-domain logits (softmax) or natural logits (relu)
       const float cs = (NORM == NORM_SOFTMAX) ? c2 : p.scale;
@@ -306,6 +313,7 @@ __global__ void __launch_bounds__(WAVES * 64)
             bool ok = key < p.Nkv;
             if constexpr (MASK == MASK_CAUSAL) ok = ok && key <= qrow;
             if constexpr (MASK == MASK_SW) ok = ok && abs(qrow - key) < p.window;
+            if constexpr (MASK == MASK_CSW) ok = ok && key <= qrow && qrow - key < p.window;
             s[kb][r] = ok ? s[kb][r] : -INFINITY;
           }
         }

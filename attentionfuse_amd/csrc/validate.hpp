@@ -1,0 +1,38 @@
+// Argument checks shared by the forward, decode and backward entry points.
+#pragma once
+
+#include <stdint.h>
+
+#include "attnfuse_hip.h"
+
+namespace af {
+
+void set_error(const char* fmt, ...);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// (B, H, N, D) tensor with unit D-stride and 16-byte aligned rows.
+inline int check_bhnd(const char* name, const void* ptr, const int64_t* st) {
+  if (ptr == nullptr) {
+    set_error("%s is NULL", name);
+    return AF_ERR_BAD_ARG;
+  }
+  if (st[3] != 1) {
+    set_error("%s: head-dim stride must be 1 (got %lld)", name, (long long)st[3]);
+    return AF_ERR_BAD_ARG;
+  }
+  if (!aligned16(ptr)) {
+    set_error("%s: base pointer must be 16-byte aligned", name);
+    return AF_ERR_BAD_ARG;
+  }
+  for (int i = 0; i < 3; ++i)
+    if (st[i] % 8 != 0) {
+      set_error("%s: stride[%d]=%lld is not a multiple of 8 elements", name, i, (long long)st[i]);
+      return AF_ERR_BAD_ARG;
+    }
+  return AF_OK;
+}
+
+inline bool head_dim_supported(int d) { return d == 32 || d == 64 || d == 128; }
+
+}  // namespace af

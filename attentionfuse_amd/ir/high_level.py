@@ -28,6 +28,8 @@ class MaskKind(enum.Enum):
     CAUSAL = "causal"
     SLIDING_WINDOW = "sliding_window"
     BLOCK_SPARSE = "block_sparse"
+    # produced by lowering only: causal + sliding_window (keys i-W < j <= i)
+    CAUSAL_SLIDING_WINDOW = "causal_sliding_window"
 
 
 class BiasKind(enum.Enum):

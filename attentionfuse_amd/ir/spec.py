@@ -19,7 +19,8 @@ from .high_level import BiasKind, MaskKind, NormKind
 
 DTYPE_CODES = {"float16": 0, "bfloat16": 1, "float32": 2}
 MASK_CODES = {MaskKind.FULL: 0, MaskKind.CAUSAL: 1,
-              MaskKind.SLIDING_WINDOW: 2, MaskKind.BLOCK_SPARSE: 3}
+              MaskKind.SLIDING_WINDOW: 2, MaskKind.BLOCK_SPARSE: 3,
+              MaskKind.CAUSAL_SLIDING_WINDOW: 4}
 BIAS_CODES = {None: 0, BiasKind.ALIBI: 1, BiasKind.ADDITIVE: 2}
 NORM_CODES = {NormKind.SOFTMAX: 0, NormKind.RELU: 1}
 

@@ -51,7 +51,8 @@ typedef enum af_mask {
   AF_MASK_FULL = 0,
   AF_MASK_CAUSAL = 1,          /* key j visible to query i iff j <= i        */
   AF_MASK_SLIDING_WINDOW = 2,  /* visible iff |i - j| < window               */
-  AF_MASK_BLOCK_SPARSE = 3     /* visible iff (i/BM, j/BN) is a listed tile  */
+  AF_MASK_BLOCK_SPARSE = 3,    /* visible iff (i/BM, j/BN) is a listed tile  */
+  AF_MASK_CAUSAL_SLIDING_WINDOW = 4 /* visible iff i - window < j <= i     */
 } af_mask;
 
 typedef enum af_bias {

@@ -283,6 +283,8 @@ def expected_coverage(Nq: int, Nkv: int, *, mask: str, window=None,
                 vis = k_lo <= q_hi
             elif mask == "sliding_window":
                 vis = (k_lo <= q_hi + window - 1) and (k_hi >= q_lo - window + 1)
+            elif mask == "causal_sliding_window":
+                vis = (k_lo <= q_hi) and (k_hi >= q_lo - window + 1)
             elif mask == "block_sparse":
                 vis = bool(grid[(32 * a) // bm, (64 * b) // bn])
             else:

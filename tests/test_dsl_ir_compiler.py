@@ -149,7 +149,10 @@ def test_lowering_folds_and_rejects_masks():
     def sw_causal(Q, K, V):
         return af.softmax(af.causal(af.sliding_window(af.scaled_dot_product(Q, K), 8))) @ V
     k = lower_to_tiled(_trace(sw_causal))
-    assert k.mask_kind is MaskKind.SLIDING_WINDOW and k.mask_window == 8
+    # one-sided window: keys i-W < j <= i (the reference's fold to the
+    # two-sided window changes the function)
+    assert k.mask_kind is MaskKind.CAUSAL_SLIDING_WINDOW and k.mask_window == 8
+    assert k.mask_code == 4
 
     @af.attention
     def two_bias(Q, K, V):

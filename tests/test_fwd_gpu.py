@@ -43,8 +43,10 @@ def variant(name, H, window=32, scale=None):
         return lambda Q, K, V: af.softmax(af.causal(af.alibi(af.scaled_dot_product(Q, K), H))) @ V
     if name == "additive":
         return lambda Q, K, V: af.softmax(af.additive_bias(af.scaled_dot_product(Q, K))) @ V
-    if name == "relu":
+    if name == "relu_causal":
         return lambda Q, K, V: af.relu_attention(af.causal(af.scaled_dot_product(Q, K))) @ V
+    if name == "relu":
+        return lambda Q, K, V: af.relu_attention(af.scaled_dot_product(Q, K)) @ V
     if name == "rope_causal":
         return lambda Q, K, V: af.softmax(af.causal(af.rope(Q, K))) @ V
     if name == "rope_causal_alibi":
@@ -64,7 +66,7 @@ def oracle_kwargs(name, H, Q, window=32, scale=None, bias=None, rope=None):
         kw["alibi_slopes"] = _alibi_slopes(H, "cpu", str(Q.dtype)).float()
     if name == "additive":
         kw["bias"] = bias
-    if name == "relu":
+    if name.startswith("relu"):
         kw["norm"] = "relu"
     if name.startswith("rope"):
         kw["rope"] = rope
@@ -95,7 +97,7 @@ def run_case(name, B, Hq, Hkv, N, D, dtype, Nkv=None, scale=None, seed=0):
 
 
 VARIANTS = ["dense", "causal", "sw", "sw_causal", "alibi", "causal_alibi",
-            "additive", "relu", "rope_causal", "rope_causal_alibi"]
+            "additive", "relu", "relu_causal", "rope_causal", "rope_causal_alibi"]
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
@@ -194,16 +196,18 @@ def test_deterministic():
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("mask,N", [("causal", 256), ("causal", 333), ("sw", 300), ("full", 200)])
+@pytest.mark.parametrize("mask,N", [("causal", 256), ("causal", 333), ("sw", 300), ("full", 200),
+                                    ("sw_causal", 300)])
 def test_tile_coverage_exact(mask, N):
     B, H, D, W = 2, 3, 64, 40
     Q, K, V = make(B, H, H, N, N, D, torch.float16)
-    name = {"causal": "causal", "sw": "sw", "full": "dense"}[mask]
+    name = {"causal": "causal", "sw": "sw", "full": "dense", "sw_causal": "sw_causal"}[mask]
     g = af.attention(variant(name, H, window=W))(Q, K, V, return_graph=True)
     cov = torch.zeros(B, H, -(-N // 32), -(-N // 64), dtype=torch.int32, device="cuda")
     run_attention(g, Q, K, V, coverage=cov)
     torch.cuda.synchronize()
-    want = O.expected_coverage(N, N, mask={"sw": "sliding_window"}.get(mask, mask), window=W)
+    want = O.expected_coverage(N, N, mask={"sw": "sliding_window", "sw_causal": "causal_sliding_window"}
+                               .get(mask, mask), window=W)
     assert torch.equal(cov.cpu(), want.expand(B, H, *want.shape))
 
 
