@@ -22,19 +22,23 @@ constexpr float kLn2 = 0.6931471805599453f;
 // Element types.  Data moves as raw 16-byte chunks (u32x4 = 8 elements); the
 // traits convert chunks to/from fp32 and run the matching MFMA.
 // ---------------------------------------------------------------------------
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 struct F16 {
   using T = _Float16;
   using V8 = f16x8;
+  static constexpr uint32_t kOnePair = 0x3c003c00u;   // (1.0, 1.0)
   __device__ static inline float lo(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
   }
   __device__ static inline float hi(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
   }
+  // one v_cvt_pk_f16_f32 (round to nearest even)
   __device__ static inline uint32_t pack(float a, float b) {
-    uint16_t x = __builtin_bit_cast(uint16_t, (_Float16)a);
-    uint16_t y = __builtin_bit_cast(uint16_t, (_Float16)b);
-    return (uint32_t)x | ((uint32_t)y << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
   }
   __device__ static inline uint16_t one(float a) {
     return __builtin_bit_cast(uint16_t, (_Float16)a);
@@ -52,16 +56,16 @@ struct F16 {
 struct BF16 {
   using T = __bf16;
   using V8 = bf16x8;
+  static constexpr uint32_t kOnePair = 0x3f803f80u;   // (1.0, 1.0)
   __device__ static inline float lo(uint32_t w) {
     return __builtin_bit_cast(float, w << 16);
   }
   __device__ static inline float hi(uint32_t w) {
     return __builtin_bit_cast(float, w & 0xffff0000u);
   }
+  // one v_cvt_pk_bf16_f32 (round to nearest even)
   __device__ static inline uint32_t pack(float a, float b) {
-    uint16_t x = __builtin_bit_cast(uint16_t, (__bf16)a);
-    uint16_t y = __builtin_bit_cast(uint16_t, (__bf16)b);
-    return (uint32_t)x | ((uint32_t)y << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
   }
   __device__ static inline uint16_t one(float a) {
     return __builtin_bit_cast(uint16_t, (__bf16)a);
@@ -126,6 +130,54 @@ __device__ __forceinline__ float xor32(float x) {
   return __shfl_xor(x, 32, 64);
 }
 
+// max(x[l], x[l ^ 32]) with one v_permlane32_swap (no LDS round trip): the
+// swap of a register with itself returns {x[l], x[l^32]} in some order.
+__device__ __forceinline__ float max_xor32(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+
+// ---------------------------------------------------------------------------
+// Buffer resources: raw (stride 0) buffers whose num_records bounds every
+// load -- an offset at or past the end (or "negative", i.e. huge unsigned)
+// returns zeros, so tile loads need neither clamps nor branches.
+// ---------------------------------------------------------------------------
+constexpr int kBufferWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, kBufferWord3);
+}
+__device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Transposed LDS read (ds_read_b64_tr_b16).  Within each 16-lane group,
+// result lane L, element i is element (L % 4) of the 64-bit chunk addressed
+// by source lane (L % 16) / 4 + 4 i.  Two reads therefore build the
+// 32x32x16 A operand "row d, k-slots = 8 consecutive rows of a row-major
+// tile" that an MFMA needs for V^T without a transposed copy in LDS; see
+// tr_source_offset for the per-lane address.
+// ---------------------------------------------------------------------------
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// Element offset (within a row-major tile of pitch `pitch`) that source lane
+// `lane` must address so that, after two ds_read_b64_tr_b16 (t = 0, 1), the
+// wave holds the A operand X^T[32 db + l%32][keys 16 kk + 8 h + (0..7)] of a
+// 32x32x16 MFMA, X being the (keys x dims) tile.
+__device__ __forceinline__ int tr_source_offset(int lane, int t, int pitch) {
+  const int row = 8 * (lane >> 5) + 4 * t + ((lane & 15) >> 2);
+  const int col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  return row * pitch + col;
+}
+
 // ---------------------------------------------------------------------------
 // RoPE, rotate-half convention (reference: attnfuse/rope_utils.py:57-73):
 //   out[d]       = x[d] cos[d]       - x[d+D/2] sin[d]
@@ -136,21 +188,45 @@ __device__ __forceinline__ float xor32(float x) {
 // ---------------------------------------------------------------------------
 template <class E>
 __device__ inline void rope_pair(u32x4& lo, u32x4& hi, u32x4 clo, u32x4 slo,
-                                 u32x4 chi, u32x4 shi) {
+                                 u32x4 chi, u32x4 shi);
+
+// fp16: written on half vectors so the compiler emits mixed-precision FMAs
+// (f16 operands, exact f32 product and sum, one rounding to f16).
+template <>
+__device__ inline void rope_pair<F16>(u32x4& lo, u32x4& hi, u32x4 clo, u32x4 slo,
+                                      u32x4 chi, u32x4 shi) {
+  const f16x8 xl = __builtin_bit_cast(f16x8, lo), xh = __builtin_bit_cast(f16x8, hi);
+  const f16x8 cl = __builtin_bit_cast(f16x8, clo), sl = __builtin_bit_cast(f16x8, slo);
+  const f16x8 ch = __builtin_bit_cast(f16x8, chi), sh = __builtin_bit_cast(f16x8, shi);
+  f16x8 ol, oh;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float a = __builtin_fmaf((float)xh[i], -(float)sl[i], 0.f);
+    const float b = __builtin_fmaf((float)xl[i], (float)sh[i], 0.f);
+    ol[i] = (_Float16)__builtin_fmaf((float)xl[i], (float)cl[i], a);
+    oh[i] = (_Float16)__builtin_fmaf((float)xh[i], (float)ch[i], b);
+  }
+  lo = __builtin_bit_cast(u32x4, ol);
+  hi = __builtin_bit_cast(u32x4, oh);
+}
+
+template <>
+__device__ inline void rope_pair<BF16>(u32x4& lo, u32x4& hi, u32x4 clo, u32x4 slo,
+                                       u32x4 chi, u32x4 shi) {
   float xl[8], xh[8], cl[8], sl[8], ch[8], sh[8], ol[8], oh[8];
-  unpack8<E>(lo, xl);
-  unpack8<E>(hi, xh);
-  unpack8<E>(clo, cl);
-  unpack8<E>(slo, sl);
-  unpack8<E>(chi, ch);
-  unpack8<E>(shi, sh);
+  unpack8<BF16>(lo, xl);
+  unpack8<BF16>(hi, xh);
+  unpack8<BF16>(clo, cl);
+  unpack8<BF16>(slo, sl);
+  unpack8<BF16>(chi, ch);
+  unpack8<BF16>(shi, sh);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     ol[i] = xl[i] * cl[i] - xh[i] * sl[i];
     oh[i] = xh[i] * ch[i] + xl[i] * sh[i];
   }
-  lo = pack8<E>(ol);
-  hi = pack8<E>(oh);
+  lo = pack8<BF16>(ol);
+  hi = pack8<BF16>(oh);
 }
 
 // Inverse (transpose) rotation applied to a gradient g of the rotated vector:

@@ -119,12 +119,24 @@ FwdParams make_fwd_params(const af_fwd_args* a, int bm) {
   p.n_mblocks = (a->seqlen_q + bm - 1) / bm;
   p.cov_nq = (a->seqlen_q + 31) / 32;
   p.cov_nk = (a->seqlen_kv + kKeysPerStage - 1) / kKeysPerStage;
+  p.rope_len = a->rope_len;
   p.scale = a->scale;
   p.window = a->window;
   return p;
 }
 
+// The kernels address each (batch, head) slice of K, V and the RoPE tables
+// through a raw buffer resource with a 32-bit byte range.
+bool slice_fits_u32(int64_t rows, int64_t row_stride, int d) {
+  return rows <= 0 || ((rows - 1) * row_stride + d) * 2 < (int64_t(1) << 32);
+}
+
 int dispatch_fwd(const FwdParams& p, const af_spec_key& k, int waves, hipStream_t s) {
+  if (!slice_fits_u32(p.Nkv, p.ks[2], k.head_dim) || !slice_fits_u32(p.Nkv, p.vs[2], k.head_dim) ||
+      (k.rope && !slice_fits_u32(p.rope_len, p.rs[0], k.head_dim)))
+    return fail(AF_ERR_UNSUPPORTED, "a (batch, head) slice of K, V or the RoPE tables spans 4 GiB or more");
+  if (!(p.scale > 0.f) || p.scale == INFINITY)
+    return fail(AF_ERR_BAD_ARG, "scale must be positive and finite (got %g)", (double)p.scale);
   const dim3 grid((unsigned)p.n_mblocks * (unsigned)(p.B * p.Hq));
   int rc = -1;
   const bool f16 = k.dtype == AF_F16;

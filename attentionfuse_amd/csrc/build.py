@@ -28,6 +28,9 @@ ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep MFMA accumulators in VGPRs: VALU work on them (the softmax
+    # rescale) then needs no AGPR<->VGPR copies around the loop
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     f"-I{ROOT / 'include'}", f"-I{HERE}", "-Wno-unused-result",
 ]
 

@@ -11,14 +11,19 @@
 // Work decomposition (MI355X-first, not a translation):
 //  * a workgroup owns BM = 32*WAVES query rows of one (batch, head); each
 //    wave64 owns 32 rows: one 32x32 MFMA output block.
-//  * K and V stream through LDS in 64-key stages, double-buffered: global
+//  * K and V stream through LDS in 64-key stages, double-buffered: buffer
 //    loads for stage t+1 are in flight while stage t is on the MFMA pipes.
+//    The loads go through raw buffer resources, so rows past N_kv come back
+//    as zeros from the hardware bounds check (no clamps, no branches).
 //    K is rotated (RoPE) once per stage while it is written to LDS; V is
-//    written transposed (V^T) so that the P*V MFMA reads 16-byte rows.
+//    written row-major and read back transposed by ds_read_b64_tr_b16.
 //  * scores are computed transposed (S^T = K Q^T): each lane then holds 32
-//    keys of one query, so the row max / row sum are in-register plus one
-//    exchange with lane ^ 32, and P^T is the B operand of the P*V MFMA
-//    without any register shuffle (see af_common.hpp).
+//    keys of one query, so the row max is in-register plus one
+//    v_permlane32_swap, and P^T is the B operand of the P*V MFMA without any
+//    register shuffle (see af_common.hpp).  Row sums come from the MFMA pipe
+//    (an all-ones A operand times P^T).
+//  * the softmax max is lazy: the running max only moves when a score
+//    exceeds it by more than 2^kTau, so the O rescale is rare.
 //  * Q stays in registers for the whole kernel, rotated once.
 //  * causal grids run the longest query blocks first.
 #pragma once
@@ -51,9 +56,18 @@ struct FwdParams {
   int32_t B, Hq, Hkv, Nq, Nkv, G;
   int32_t n_mblocks, bs_block_n;
   int32_t cov_nq, cov_nk;
+  int32_t rope_len;
   float scale;
   int32_t window;
 };
+
+// Row pitch (elements) of the row-major V stage: D/2 + 16 dwords (16 when
+// D = 32), i.e. 16 mod 32 dwords, so the eight rows one transposed read
+// touches spread over all 64 banks exactly twice.
+template <int D>
+constexpr int v_pitch() {
+  return D == 32 ? 32 : D + 32;
+}
 
 template <class E, int D, int MASK, int BIAS, int NORM, bool ROPE, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64)
@@ -61,17 +75,17 @@ __global__ void __launch_bounds__(WAVES * 64)
   constexpr int NT = WAVES * 64;
   constexpr int BM = 32 * WAVES;
   constexpr int BN = 64;
-  constexpr int KP = D + 8;    // K stage row pitch (elements)
-  constexpr int VP = BN + 8;   // V^T stage row pitch (elements)
-  constexpr int KS = D / 16;   // 16-deep k-steps of Q K^T
-  constexpr int DB = D / 32;   // 32-row blocks of O^T
-  constexpr int STAGE = BN * KP + D * VP;  // elements per LDS stage
+  constexpr int KP = D + 8;          // K stage row pitch (elements)
+  constexpr int VP = v_pitch<D>();   // V stage row pitch (elements)
+  constexpr int KS = D / 16;         // 16-deep k-steps of Q K^T
+  constexpr int DB = D / 32;         // 32-row blocks of O^T
+  constexpr int STAGE = BN * KP + BN * VP;  // elements per LDS stage
   // K staging: rotate-half pairs (chunk j, chunk j + D/16) of one key row.
   constexpr int KPAIRS = BN * D / 16;
   constexpr int KPT = (KPAIRS + NT - 1) / NT;
-  // V staging: units of 2 keys x 8 dims, written to V^T as packed pairs.
-  constexpr int VUNITS = (BN / 2) * (D / 8);
-  constexpr int VPT = (VUNITS + NT - 1) / NT;
+  // V staging: 16-byte chunks of the row-major tile.
+  constexpr int VCHUNKS = BN * D / 8;
+  constexpr int VPT = (VCHUNKS + NT - 1) / NT;
 
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
 
@@ -84,7 +98,8 @@ __global__ void __launch_bounds__(WAVES * 64)
   const int BH = p.B * p.Hq;
   const int bh = blockIdx.x % BH;
   const int mbi = blockIdx.x / BH;
-  const int mb = (MASK == MASK_CAUSAL) ? (p.n_mblocks - 1 - mbi) : mbi;
+  const bool heavy_last = MASK == MASK_CAUSAL || MASK == MASK_CSW;
+  const int mb = heavy_last ? (p.n_mblocks - 1 - mbi) : mbi;
   const int b = bh / p.Hq;
   const int hq = bh - b * p.Hq;
   const int hk = hq / p.G;
@@ -93,8 +108,8 @@ __global__ void __launch_bounds__(WAVES * 64)
   const int qrow = q0w + c;
 
   const uint16_t* __restrict__ qbase = p.q + b * p.qs[0] + hq * p.qs[1];
-  const uint16_t* __restrict__ kbase = p.k + b * p.ks[0] + hk * p.ks[1];
-  const uint16_t* __restrict__ vbase = p.v + b * p.vs[0] + hk * p.vs[1];
+  const uint16_t* kbase = p.k + b * p.ks[0] + hk * p.ks[1];
+  const uint16_t* vbase = p.v + b * p.vs[0] + hk * p.vs[1];
   const int64_t kstr = p.ks[2], vstr = p.vs[2];
   const int64_t rstr = p.rs[0];
 
@@ -151,44 +166,48 @@ __global__ void __launch_bounds__(WAVES * 64)
     }
   };
 
-  // ---- staging registers --------------------------------------------------
+  // ---- staging through buffer resources ------------------------------------
+  // num_records covers rows [0, N_kv) of this (batch, kv head): any row
+  // outside loads as zeros (and its scores are masked anyway).
+  const uint32_t kbytes = p.Nkv > 0 ? (uint32_t)(((int64_t)(p.Nkv - 1) * kstr + D) * 2) : 0u;
+  const uint32_t vbytes = p.Nkv > 0 ? (uint32_t)(((int64_t)(p.Nkv - 1) * vstr + D) * 2) : 0u;
+  const auto krs = make_rsrc(kbase, kbytes);
+  const auto vrs = make_rsrc(vbase, vbytes);
+  const uint32_t rbytes = ROPE ? (uint32_t)(((int64_t)(p.rope_len - 1) * rstr + D) * 2) : 0u;
+  const auto crs = make_rsrc(p.cos, rbytes);
+  const auto srs = make_rsrc(p.sin, rbytes);
+
   u32x4 kr[KPT][2];
   u32x4 kc[ROPE ? KPT : 1][2], ksn[ROPE ? KPT : 1][2];
-  u32x4 vr[VPT][2];
+  u32x4 vr[VPT];
 
   auto stage_load = [&](int n0) {
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-      const int pi = tid + i * NT;
+      const int pi = min(tid + i * NT, KPAIRS - 1);
       const int row = pi / (D / 16), j = pi % (D / 16);
       const int n = n0 + row;
-      const bool ok = (KPAIRS % NT == 0 || pi < KPAIRS) && n >= 0 && n < p.Nkv;
-      const uint16_t* kp = kbase + n * kstr + 8 * j;
-      kr[i][0] = ok ? ld16(kp) : u32x4{0, 0, 0, 0};
-      kr[i][1] = ok ? ld16(kp + D / 2) : u32x4{0, 0, 0, 0};
+      const uint32_t ko = (uint32_t)((n * kstr + 8 * j) * 2);
+      kr[i][0] = buf_ld16(krs, ko);
+      kr[i][1] = buf_ld16(krs, ko + D);
       if constexpr (ROPE) {
-        const uint16_t* cp = p.cos + n * rstr + 8 * j;
-        const uint16_t* sp = p.sin + n * rstr + 8 * j;
-        kc[i][0] = ok ? ld16(cp) : u32x4{0, 0, 0, 0};
-        kc[i][1] = ok ? ld16(cp + D / 2) : u32x4{0, 0, 0, 0};
-        ksn[i][0] = ok ? ld16(sp) : u32x4{0, 0, 0, 0};
-        ksn[i][1] = ok ? ld16(sp + D / 2) : u32x4{0, 0, 0, 0};
+        const uint32_t co = (uint32_t)((n * rstr + 8 * j) * 2);
+        kc[i][0] = buf_ld16(crs, co);
+        kc[i][1] = buf_ld16(crs, co + D);
+        ksn[i][0] = buf_ld16(srs, co);
+        ksn[i][1] = buf_ld16(srs, co + D);
       }
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      const int u = tid + i * NT;
-      const int dc = u % (D / 8), kg = u / (D / 8);
-      const int n = n0 + 2 * kg;
-      const bool ok = VUNITS % NT == 0 || u < VUNITS;
-      const uint16_t* vp = vbase + n * vstr + 8 * dc;
-      vr[i][0] = (ok && n >= 0 && n < p.Nkv) ? ld16(vp) : u32x4{0, 0, 0, 0};
-      vr[i][1] = (ok && n >= 0 && n + 1 < p.Nkv) ? ld16(vp + vstr) : u32x4{0, 0, 0, 0};
+      const int u = min(tid + i * NT, VCHUNKS - 1);
+      const int row = u / (D / 8), ch = u % (D / 8);
+      vr[i] = buf_ld16(vrs, (uint32_t)(((n0 + row) * vstr + 8 * ch) * 2));
     }
   };
   auto stage_store = [&](uint16_t* buf) {
     uint16_t* Ks = buf;
-    uint16_t* Vt = buf + BN * KP;
+    uint16_t* Vs = buf + BN * KP;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int pi = tid + i * NT;
@@ -203,31 +222,46 @@ __global__ void __launch_bounds__(WAVES * 64)
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int u = tid + i * NT;
-      if (VUNITS % NT == 0 || u < VUNITS) {
-        const int dc = u % (D / 8), kg = u / (D / 8);
-        uint32_t* vt32 = reinterpret_cast<uint32_t*>(Vt);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t a = vr[i][0][e >> 1], bq = vr[i][1][e >> 1];
-          const uint32_t word = (e & 1) ? ((a >> 16) | (bq & 0xffff0000u))
-                                        : ((a & 0xffffu) | (bq << 16));
-          vt32[((8 * dc + e) * VP + 2 * kg) >> 1] = word;
-        }
+      if (VCHUNKS % NT == 0 || u < VCHUNKS) {
+        const int row = u / (D / 8), ch = u % (D / 8);
+        st16(Vs + row * VP + 8 * ch, vr[i]);
       }
     }
   };
 
   // ---- online-softmax state ------------------------------------------------
+  // Softmax runs in log2 units with a *lazy* running max: a row's m only
+  // moves when a new score exceeds it by more than kTau, so P = 2^(x - m)
+  // stays <= 2^kTau (exact in fp16/bf16 up to rounding) and the O rescale
+  // (a multiply of every accumulator) is skipped on almost every tile.  Row
+  // sums come out of the MFMA pipe: an all-ones A operand times P^T gives
+  // sum_k P[k][q] in every row of a 32x32 block.
+  constexpr float kTau = 8.f;
+  constexpr float kNegBig = -1.0e30f;
   f32x16 o[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) o[db] = f32x16{};
-  float m_run = -INFINITY;   // running max, log2 units (softmax)
-  float l_run = 0.f;         // this lane's half of the row sum
+  f32x16 lacc = f32x16{};
+  float m_run = kNegBig;
   const float c2 = p.scale * kLog2e;
+  // Materialised once through an opaque move: left as a constant the
+  // compiler re-creates it every iteration in registers that collide with
+  // the O accumulators and then has to copy O around the MFMA chain.
+  uint32_t one_pair;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(one_pair) : "s"(E::kOnePair));
+  const u32x4 ones = {one_pair, one_pair, one_pair, one_pair};
   float slope2 = 0.f;
   if constexpr (BIAS == BIAS_ALIBI) slope2 = p.slopes[hq] * kLog2e;
+  // Causal-type masks: every visible key has j <= i, so -slope |i - j| =
+  // slope (j - i), linear in the key index: accumulated with one add per
+  // score while walking the lane's keys in order.
+  constexpr bool kAlibiOneSided = BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW);
   const uint16_t* brow = nullptr;
   if constexpr (BIAS == BIAS_ADD) brow = p.bias + b * p.bs[0] + hq * p.bs[1] + (int64_t)qrow * p.bs[2];
+
+  // per-lane offsets of the transposed V reads (t = 0, 1)
+  const int vtr0 = tr_source_offset(lane, 0, VP);
+  const int vtr1 = tr_source_offset(lane, 1, VP);
 
   if (ntiles > 0) {
     stage_load(tile_n0(0));
@@ -240,7 +274,7 @@ __global__ void __launch_bounds__(WAVES * 64)
     const bool more = t + 1 < ntiles;
     if (more) stage_load(tile_n0(t + 1));
     const uint16_t* Ks = lds + (t & 1) * STAGE;
-    const uint16_t* Vt = Ks + BN * KP;
+    const uint16_t* Vs = Ks + BN * KP;
 
     bool active = q0w < p.Nq && n0 >= 0 && n0 < p.Nkv;
     if constexpr (MASK == MASK_CAUSAL) active = active && n0 <= q0w + 31;
@@ -249,11 +283,14 @@ __global__ void __launch_bounds__(WAVES * 64)
     if constexpr (MASK == MASK_CSW)
       active = active && n0 + BN - 1 > q0w - p.window && n0 <= q0w + 31;
 
-    if (active) {
-      if (p.coverage != nullptr && lane == 0) {
-        const int64_t ci = ((int64_t)(b * p.Hq + hq) * p.cov_nq + (q0w >> 5)) * p.cov_nk + (n0 >> 6);
-        atomicAdd(p.coverage + ci, 1u);
-      }
+    // A wave whose rows see nothing of this stage still runs it (all its
+    // scores are masked, so P = 0 and O, l are unchanged): a branch around
+    // the MFMAs would force the accumulators through copies every iteration.
+    if (active && p.coverage != nullptr && lane == 0) {
+      const int64_t ci = ((int64_t)(b * p.Hq + hq) * p.cov_nq + (q0w >> 5)) * p.cov_nk + (n0 >> 6);
+      atomicAdd(p.coverage + ci, 1u);
+    }
+    {
       // S^T = K Q^T over this stage: two 32-key blocks.
       f32x16 s[BN / 32];
 #pragma unroll
@@ -265,19 +302,21 @@ __global__ void __launch_bounds__(WAVES * 64)
           s[kb] = E::mfma32(ld16(krow + 16 * ks), qf[ks], s[kb]);
       }
 
-      bool need_mask = n0 + BN > p.Nkv;
+      bool need_mask = !active || n0 + BN > p.Nkv;
       if constexpr (MASK == MASK_CAUSAL) need_mask = need_mask || n0 + BN - 1 > q0w;
       if constexpr (MASK == MASK_SW)
         need_mask = need_mask || (q0w + 31 - n0 >= p.window) || (n0 + BN - 1 - q0w >= p.window);
       if constexpr (MASK == MASK_CSW)
         need_mask = need_mask || (q0w + 31 - n0 >= p.window) || n0 + BN - 1 > q0w;
 
-      // scores -> log2-domain logits (softmax) or natural logits (relu)
-      const float cs = (NORM == NORM_SOFTMAX) ? c2 : p.scale;
-      const float bscale = (NORM == NORM_SOFTMAX) ? kLog2e : 1.f;
+      // Logit of element r: s[r] * zc + zoff (log2 units for softmax,
+      // natural units for relu).
+      float zc = (NORM == NORM_SOFTMAX) ? c2 : p.scale;
+      const float zoff = 0.f;
+      if constexpr (BIAS == BIAS_ADD) {
+        const float bscale = (NORM == NORM_SOFTMAX) ? kLog2e : 1.f;
 #pragma unroll
-      for (int kb = 0; kb < BN / 32; ++kb) {
-        if constexpr (BIAS == BIAS_ADD) {
+        for (int kb = 0; kb < BN / 32; ++kb)
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             const int key0 = n0 + 32 * kb + 16 * j + 8 * h;
@@ -292,21 +331,38 @@ __global__ void __launch_bounds__(WAVES * 64)
               }
             }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) s[kb][8 * j + e] = s[kb][8 * j + e] * cs + bv[e] * bscale;
+            for (int e = 0; e < 8; ++e) s[kb][8 * j + e] = __builtin_fmaf(s[kb][8 * j + e], zc, bv[e] * bscale);
           }
+        zc = 1.f;
+      } else if constexpr (BIAS == BIAS_ALIBI) {
+        const float sl = (NORM == NORM_SOFTMAX) ? slope2 : slope2 * kLn2;
+        if constexpr (kAlibiOneSided) {
+          // keys of register r: n0 + 32 kb + 16 (r/8) + 8h + (r%8)
+#pragma unroll
+          for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              float bias = sl * (float)(n0 + 32 * kb + 16 * j + 8 * h - qrow);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                s[kb][8 * j + e] = __builtin_fmaf(s[kb][8 * j + e], zc, bias);
+                bias += sl;
+              }
+            }
         } else {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) s[kb][r] *= cs;
-        }
-        if constexpr (BIAS == BIAS_ALIBI) {
-          const float sl = (NORM == NORM_SOFTMAX) ? slope2 : slope2 * kLn2;
+          for (int kb = 0; kb < BN / 32; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = n0 + 32 * kb + acc_key(r, h);
-            s[kb][r] -= sl * (float)abs(qrow - key);
-          }
+            for (int r = 0; r < 16; ++r) {
+              const int key = n0 + 32 * kb + acc_key(r, h);
+              s[kb][r] = __builtin_fmaf(s[kb][r], zc, -sl * (float)abs(qrow - key));
+            }
         }
-        if (need_mask) {
+        zc = 1.f;
+      }
+      if (need_mask) {
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = n0 + 32 * kb + acc_key(r, h);
@@ -316,42 +372,37 @@ __global__ void __launch_bounds__(WAVES * 64)
             if constexpr (MASK == MASK_CSW) ok = ok && key <= qrow && qrow - key < p.window;
             s[kb][r] = ok ? s[kb][r] : -INFINITY;
           }
-        }
       }
 
-      float alpha = 1.f;
       if constexpr (NORM == NORM_SOFTMAX) {
-        float mx = -INFINITY;
+        float mz = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < BN / 32; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-        mx = fmaxf(mx, xor32(mx));
-        const float m_new = fmaxf(m_run, mx);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        float ls = 0.f;
+          for (int r = 0; r < 16; ++r) mz = fmaxf(mz, s[kb][r]);
+        const float mx = max_xor32(__builtin_fmaf(mz, zc, zoff));
+        // alpha is 1 unless this row's max grew past the slack; the multiply
+        // runs unconditionally because a branch around it makes the register
+        // allocator copy every accumulator at the loop back-edge.
+        const bool grow = mx > m_run + kTau;
+        {
+          const float m_new = grow ? mx : m_run;
+          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+          for (int db = 0; db < DB; ++db) o[db] *= alpha;
+          lacc *= alpha;
+          m_run = m_new;
+        }
+        const float off = zoff - m_run;
 #pragma unroll
         for (int kb = 0; kb < BN / 32; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float pv = __builtin_amdgcn_exp2f(s[kb][r] - m_use);
-            s[kb][r] = pv;
-            ls += pv;
-          }
-        l_run = l_run * alpha + ls;
-        m_run = m_new;
+          for (int r = 0; r < 16; ++r) s[kb][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], zc, off));
       } else {
-        float ls = 0.f;
 #pragma unroll
         for (int kb = 0; kb < BN / 32; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float pv = fmaxf(s[kb][r], 0.f);
-            s[kb][r] = pv;
-            ls += pv;
-          }
-        l_run += ls;
+          for (int r = 0; r < 16; ++r) s[kb][r] = fmaxf(__builtin_fmaf(s[kb][r], zc, zoff), 0.f);
       }
 
       // P^T (registers) -> B operands, one per 16 keys.
@@ -364,12 +415,17 @@ __global__ void __launch_bounds__(WAVES * 64)
           pf[kk][i] = E::pack(s[kb][8 * j + 2 * i], s[kb][8 * j + 2 * i + 1]);
       }
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        if constexpr (NORM == NORM_SOFTMAX) o[db] *= alpha;
-        const uint16_t* vrow = Vt + (32 * db + c) * VP + 8 * h;
+      for (int kk = 0; kk < BN / 16; ++kk) lacc = E::mfma32(ones, pf[kk], lacc);
 #pragma unroll
-        for (int kk = 0; kk < BN / 16; ++kk)
-          o[db] = E::mfma32(ld16(vrow + 16 * kk), pf[kk], o[db]);
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int kk = 0; kk < BN / 16; ++kk) {
+          const uint16_t* vt = Vs + 16 * kk * VP + 32 * db;
+          const u32x2 lo = lds_read_tr16(vt + vtr0);
+          const u32x2 hi = lds_read_tr16(vt + vtr1);
+          const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
+          o[db] = E::mfma32(va, pf[kk], o[db]);
+        }
       }
     }
 
@@ -378,7 +434,8 @@ __global__ void __launch_bounds__(WAVES * 64)
   }
 
   // ---- epilogue -------------------------------------------------------------
-  const float lt = l_run + xor32(l_run);
+  // every register of lacc holds this lane's query row sum
+  const float lt = lacc[0];
   const float inv = (lt == 0.f) ? 1.f : 1.f / lt;
   if (qrow < p.Nq) {
     uint16_t* orow = p.o + b * p.os[0] + hq * p.os[1] + (int64_t)qrow * p.os[2];
@@ -393,10 +450,10 @@ __global__ void __launch_bounds__(WAVES * 64)
         *reinterpret_cast<u32x2*>(orow + d0) = w2;
       }
     if (p.lse != nullptr && h == 0) {
-      const float ll = (lt == 0.f) ? 1.f : lt;
-      float L;
-      if constexpr (NORM == NORM_SOFTMAX) L = (m_run + __log2f(ll)) * kLn2;
-      else L = -INFINITY;
+      float L = -INFINITY;
+      if constexpr (NORM == NORM_SOFTMAX) {
+        if (lt > 0.f) L = (m_run + __log2f(lt)) * kLn2;
+      }
       p.lse[b * p.ls[0] + hq * p.ls[1] + (int64_t)qrow * p.ls[2]] = L;
     }
   }

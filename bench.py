@@ -155,6 +155,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-alibi", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: the fused-attention kernels run on "
@@ -167,8 +168,10 @@ def main():
     ms, tensors = bench_forward(args.steps, args.warmup, alibi=False)
     flops = causal_flops(**C2)
     tflops = flops / (ms * 1e-3) / 1e12
-    ms_alibi, _ = bench_forward(args.steps, args.warmup, alibi=True)
-    tflops_alibi = flops / (ms_alibi * 1e-3) / 1e12
+    ms_alibi = tflops_alibi = None
+    if not args.no_alibi:
+        ms_alibi, _ = bench_forward(args.steps, args.warmup, alibi=True)
+        tflops_alibi = flops / (ms_alibi * 1e-3) / 1e12
 
     line = {
         "metric": "fwd TFLOPS (causal+RoPE, N=4096) + decode HBM GB/s (Llama-3-8B GQA 32k)",
@@ -194,9 +197,10 @@ def main():
                      "traffic": None,
                      "kernel": "fwd_kernel<F16,64,CAUSAL,NONE,SOFTMAX,ROPE,4>",
                      "algorithmic_flop_per_launch": flops},
-        "alibi": {"ms": round(ms_alibi, 5), "tflops": round(tflops_alibi, 3),
-                  "frac": round(tflops_alibi / PEAK_FP16_TFLOPS, 4)},
     }
+    if ms_alibi is not None:
+        line["alibi"] = {"ms": round(ms_alibi, 5), "tflops": round(tflops_alibi, 3),
+                         "frac": round(tflops_alibi / PEAK_FP16_TFLOPS, 4)}
     if not args.no_decode:
         ms_dec = bench_decode(args.steps, args.warmup)
         nbytes = decode_bytes(**{k: C3[k] for k in ("B", "Hq", "Hkv", "N", "D")})
