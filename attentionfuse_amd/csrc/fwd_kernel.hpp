@@ -113,7 +113,12 @@ __global__ void __launch_bounds__(WAVES * 64)
   const int64_t kstr = p.ks[2], vstr = p.vs[2];
   const int64_t rstr = p.rs[0];
 
+  const float c2 = p.scale * kLog2e;
+
   // ---- Q fragment (B operand of S^T = K Q^T), rotated once -------------
+  // The rotated q~ is rounded to 16 bits unscaled, as the reference kernel
+  // rounds it (attnfuse/compiler/codegen.py:126-135); the softmax scale is
+  // applied to the fp32 scores.
   u32x4 qf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
@@ -243,7 +248,6 @@ __global__ void __launch_bounds__(WAVES * 64)
   for (int db = 0; db < DB; ++db) o[db] = f32x16{};
   f32x16 lacc = f32x16{};
   float m_run = kNegBig;
-  const float c2 = p.scale * kLog2e;
   // Materialised once through an opaque move: left as a constant the
   // compiler re-creates it every iteration in registers that collide with
   // the O accumulators and then has to copy O around the MFMA chain.
@@ -381,16 +385,34 @@ __global__ void __launch_bounds__(WAVES * 64)
 #pragma unroll
           for (int r = 0; r < 16; ++r) mz = fmaxf(mz, s[kb][r]);
         const float mx = max_xor32(__builtin_fmaf(mz, zc, zoff));
-        // alpha is 1 unless this row's max grew past the slack; the multiply
-        // runs unconditionally because a branch around it makes the register
-        // allocator copy every accumulator at the loop back-edge.
+        // The rescale runs only when some row of the wave grew past the
+        // slack.  It multiplies the accumulators in place (tied asm
+        // operands): written as plain C++ inside the branch, the register
+        // allocator gives the two paths different registers and copies every
+        // accumulator on every iteration.  The s_nops give the MFMA->VALU
+        // and VALU->MFMA dependencies on the accumulators their wait states,
+        // which the hazard recognizer cannot see through the asm; alpha is an
+        // operand of the nops so its v_exp is issued before them.
         const bool grow = mx > m_run + kTau;
-        {
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
           const float m_new = grow ? mx : m_run;
           const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+          asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : : "v"(alpha));
 #pragma unroll
-          for (int db = 0; db < DB; ++db) o[db] *= alpha;
-          lacc *= alpha;
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              float x = o[db][r];
+              asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x) : "v"(alpha));
+              o[db][r] = x;
+            }
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float x = lacc[r];
+            asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x) : "v"(alpha));
+            lacc[r] = x;
+          }
+          asm volatile("s_nop 7");
           m_run = m_new;
         }
         const float off = zoff - m_run;

@@ -117,11 +117,15 @@ def naive_attention(Q, K, V, *, causal: bool = False, window=None,
                     alibi_slopes=None, scale: Optional[float] = None,
                     elem_mask=None, bias=None, norm: str = "softmax",
                     rope=None, query_offset: int = 0,
-                    dtype=torch.float32, return_lse: bool = False):
+                    dtype=torch.float32, return_lse: bool = False,
+                    rope_round=None):
     """Reference attention on upcast CPU copies.
 
     Q (B, Hq, Nq, D); K, V (B, Hkv, Nkv, D) with Hq % Hkv == 0.
     ``rope`` = (cos, sin) tables, applied to Q and K at positions 0..N-1.
+    ``rope_round`` -- optional 16-bit dtype the rotated q~, k~ are rounded to
+    before the dot product, as the reference kernel does
+    (attnfuse/compiler/codegen.py:126-135,195-204).
     Returns O (B, Hq, Nq, D) in ``dtype`` (and L (B, Hq, Nq) if asked)."""
     Q = Q.detach().to("cpu", dtype) if not Q.requires_grad else Q.to(dtype)
     K = K.detach().to("cpu", dtype) if not K.requires_grad else K.to(dtype)
@@ -132,6 +136,9 @@ def naive_attention(Q, K, V, *, causal: bool = False, window=None,
         cos, sin = (t.to("cpu", dtype) for t in rope)
         Q = apply_rope(Q, cos, sin, torch.arange(Nq) + query_offset)
         K = apply_rope(K, cos, sin)
+        if rope_round is not None:
+            Q = Q.to(rope_round).to(dtype)
+            K = K.to(rope_round).to(dtype)
     K, V = expand_kv(K, G), expand_kv(V, G)
     Nkv = K.shape[2]
     sc = 1.0 / math.sqrt(D) if scale is None else scale

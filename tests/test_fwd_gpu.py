@@ -211,6 +211,45 @@ def test_tile_coverage_exact(mask, N):
     assert torch.equal(cov.cpu(), want.expand(B, H, *want.shape))
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("pattern", ["ramp", "spike_late", "spike_early", "ramp_down"])
+@pytest.mark.parametrize("name", ["causal", "dense", "rope_causal", "rope_causal_alibi"])
+def test_online_softmax_rescale_paths(name, pattern, dtype):
+    """Scores that grow along the key axis force the running max to move
+    after the first stage (the rescale path random inputs almost never
+    reach); a large early score exercises the path that never rescales."""
+    B, H, N, D = 1, 4, 512, 64
+    Q, K, V = make(B, H, H, N, N, D, dtype, seed=11)
+    j = torch.arange(N, device="cuda", dtype=torch.float32)
+    if pattern == "ramp":
+        K = (K.float() * (1 + 6 * j / N)[None, None, :, None]).to(dtype)
+    elif pattern == "ramp_down":
+        K = (K.float() * (7 - 6 * j / N)[None, None, :, None]).to(dtype)
+    elif pattern == "spike_late":
+        K[:, :, N - 70] = (K[:, :, N - 70].float() * 25).to(dtype)
+        K[:, :, 300] = (K[:, :, 300].float() * 12).to(dtype)
+    else:
+        K[:, :, 3] = (K[:, :, 3].float() * 25).to(dtype)
+    fn = af.attention(variant(name, H))
+    extra, rope = {}, None
+    if name.startswith("rope"):
+        cos, sin = build_rope_cache(N, D, device="cuda", dtype=dtype)
+        extra = {"cos": cos, "sin": sin}
+        rope = (cos[0, 0].cpu(), sin[0, 0].cpu())
+    L = torch.empty(B, H, N, dtype=torch.float32, device="cuda")
+    g = fn(Q, K, V, return_graph=True)
+    out = run_attention(g, Q, K, V, save_lse=L, **extra)
+    torch.cuda.synchronize()
+    # keys up to 25x N(0,1): the rotated k~ rounding to 16 bits (the
+    # reference kernel's semantics) dominates, so the oracle rounds it too
+    want, Lw = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(), return_lse=True,
+                                 rope_round=dtype if rope is not None else None,
+                                 **oracle_kwargs(name, H, Q, rope=rope))
+    assert (out.float().cpu() - want).abs().max().item() <= TOL[dtype]
+    # L grows with the scores; compare relative to its size
+    assert ((L.cpu() - Lw).abs() / Lw.abs().clamp(min=1)).max().item() <= LSE_TOL[dtype]
+
+
 def test_smoke_dense_matches_reference_test():
     """Reference tests/test_smoke.py::test_dispatch_dense_gpu."""
     fn = af.attention(variant("dense", 2))
