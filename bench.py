@@ -1,32 +1,45 @@
 """Benchmark of the fused-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--no-cpu] [--no-decode] [--no-alibi] [--no-train]
+    python bench.py --copy-calibration      # plain copy, for HBM counters
 
 A step is one fused forward over config 2 of the benchmark configs: causal +
 RoPE (base 1e4, rotate-half), fp16, B=4, H=12, N=4096, D=64, scale 1/8,
 Q/K/V ~ N(0,1) from seed 0 -- the headline "fwd TFLOPS (causal+RoPE,
 N=4096)".  ``value`` is algorithmic TFLOP/s: 4*B*H*D*N(N+1)/2 =
 103,104,380,928 FLOP per step (unmasked causal pairs only), inputs resident in
-HBM.  The same line carries
+HBM, every step exactly one kernel launch.  The same line carries
 
 * ``roofline`` -- the forward kernel against the 2.5 PFLOP/s dense fp16
-  MFMA peak (kernel time from HIP events on the launch stream over the timed
-  region; each step is exactly one kernel launch);
+  MFMA peak; kernel time from HIP events recorded on the stream the kernel is
+  launched on, over the timed region.  ``traffic`` is HBM bytes per launch
+  from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+  (profiles/hbm_traffic_*.txt, scaled by a plain copy of known size), or
+  null when that summary is absent;
 * ``alibi`` -- the same forward with ALiBi added (config 2 as written);
 * ``decode`` -- config 3 (Llama-3-8B GQA decode, bf16, B=8, H_q=32, H_kv=8,
   D=128, cache 32768): algorithmic bytes K+V+Q+O = 1,073,872,896 per call
-  over kernel time, against 8 TB/s; two K/V cache copies alternate so no call
-  is served from the 256 MB last-level cache;
+  over kernel time (split + combine), against 8 TB/s; two K/V cache copies
+  alternate so no call is served from the 256 MB last-level cache;
+* ``bigbird`` -- config 4 (block-sparse fwd+bwd, fp16, B=4 H=12 N=4096
+  D=64, 64x64 blocks, BigBird + 3 random blocks per row from the committed
+  mask fixture): 14*B*H*D*4096*n_active FLOP per fwd+bwd step;
+* ``train`` -- config 5 (causal GQA + fused RoPE base 5e5, fwd+bwd, bf16,
+  B=1 N=4096 H_q=32 H_kv=8 D=128): 3.5 x 4*B*H_q*D*N(N+1)/2 FLOP per step;
 * ``cpu_baseline`` -- the fp32 CPU oracle (a restatement of the reference's
   naive attention) on a bounded sample of config 2's heads, on the host's
-  cores, plus the max-abs difference between the GPU output and the oracle
-  on the sampled heads.
+  cores, plus config 1 (GPT-2-small causal, B=1 H=12 N=512 D=64, fp32) in
+  full, and the max-abs difference between the GPU output and the oracle on
+  the sampled heads.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -37,8 +50,13 @@ sys.path.insert(0, str(ROOT))
 PEAK_FP16_TFLOPS = 2500.0      # MI355X dense fp16/bf16 MFMA, published
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, published
 
+C1 = dict(B=1, H=12, N=512, D=64)
 C2 = dict(B=4, H=12, N=4096, D=64)
 C3 = dict(B=8, Hq=32, Hkv=8, N=32768, D=128)
+C4 = dict(B=4, H=12, N=4096, D=64)
+C5 = dict(B=1, Hq=32, Hkv=8, N=4096, D=128)
+FWD_KERNEL = "fwd_kernel<af::F16, 64, 1, 0, 0, true, 4>"
+COPY_BYTES = 1 << 30
 
 
 def causal_flops(B, H, N, D):
@@ -49,18 +67,23 @@ def decode_bytes(B, Hq, Hkv, N, D, elem=2):
     return 2 * B * Hkv * N * D * elem + 2 * B * Hq * D * elem
 
 
-def _time_launch(launch, steps, warmup, stream_sync, events):
+def _time_launch(launch, steps, warmup):
+    """Average ms per launch() from HIP events recorded on the stream the
+    kernels are launched on (torch's current stream, which the launchers
+    pass to the C ABI)."""
     import torch
+    stream = torch.cuda.current_stream()
     for _ in range(warmup):
         launch()
     torch.cuda.synchronize()
-    start, end = events
-    start.record()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
     for _ in range(steps):
         launch()
-    end.record()
+    end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps   # ms
+    return start.elapsed_time(end) / steps
 
 
 def bench_forward(steps, warmup, alibi: bool):
@@ -83,8 +106,7 @@ def bench_forward(steps, warmup, alibi: bool):
         fn = af.attention(lambda Q, K, V: af.softmax(af.causal(af.rope(Q, K))) @ V)
     graph = fn(Q, K, V, return_graph=True)
     launch, out = prepare_attention(graph, Q, K, V, cos=cos, sin=sin)
-    ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-    ms = _time_launch(launch, steps, warmup, None, ev)
+    ms = _time_launch(launch, steps, warmup)
     return ms, (Q, K, V, cos, sin, out)
 
 
@@ -114,9 +136,105 @@ def bench_decode(steps, warmup):
     def launch():
         launches[state["i"] & 1]()
         state["i"] += 1
-    ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-    ms = _time_launch(launch, steps, warmup, None, ev)
-    return ms
+    return _time_launch(launch, steps, warmup)
+
+
+def bench_bigbird(steps, warmup):
+    """Config 4: block-sparse forward (saving the LSE) + backward."""
+    import torch
+
+    from attentionfuse_amd.runtime.block_mask import (
+        block_mask_from_blocks, run_block_sparse, run_block_sparse_backward)
+
+    fx = json.loads((ROOT / "tests" / "golden" / "bigbird_c4_grid.json").read_text())
+    n = fx["n_blocks"]
+    grid = torch.zeros(n, n, dtype=torch.bool)
+    for a, row in enumerate(fx["rows"]):
+        grid[a, row] = True
+    dev = torch.device("cuda:0")
+    B, H, N, D = C4["B"], C4["H"], C4["N"], C4["D"]
+    assert N == 64 * n
+    bm = block_mask_from_blocks(grid, 64, 64, device=dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    Q, K, V, dO = (torch.randn(B, H, N, D, generator=g, device=dev, dtype=torch.float16)
+                   for _ in range(4))
+    L = torch.empty(B, H, N, dtype=torch.float32, device=dev)
+    out = torch.empty_like(Q)
+    scale = D ** -0.5
+
+    def step():
+        run_block_sparse(Q, K, V, bm, scale, out=out, save_lse=L)
+        run_block_sparse_backward(Q, K, V, out, L, dO, bm, scale)
+    ms = _time_launch(step, steps, warmup)
+    flops = 14 * B * H * D * 64 * 64 * bm.n_active
+    return {"workload": "config 4: BigBird block-sparse fwd+bwd fp16 B=4 H=12 N=4096 D=64, "
+                        f"64x64 blocks, {bm.n_active} active of {n * n}",
+            "ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+            "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+            "algorithmic_flop_per_step": flops}
+
+
+def bench_train(steps, warmup):
+    """Config 5: causal GQA + fused RoPE (base 5e5) forward + backward."""
+    import torch
+
+    import attnfuse as af
+    from attnfuse.rope_utils import build_rope_cache
+    from attentionfuse_amd.runtime.backward import run_backward
+    from attentionfuse_amd.runtime.prepared import prepare_attention
+
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, N, D = C5["B"], C5["Hq"], C5["Hkv"], C5["N"], C5["D"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    Q = torch.randn(B, Hq, N, D, generator=g, device=dev, dtype=torch.bfloat16)
+    K = torch.randn(B, Hkv, N, D, generator=g, device=dev, dtype=torch.bfloat16)
+    V = torch.randn(B, Hkv, N, D, generator=g, device=dev, dtype=torch.bfloat16)
+    dO = torch.randn(B, Hq, N, D, generator=g, device=dev, dtype=torch.bfloat16)
+    cos, sin = build_rope_cache(N, D, base=500000.0, device=dev, dtype=torch.bfloat16)
+    fn = af.attention(lambda Q, K, V: af.softmax(af.causal(af.rope(Q, K))) @ V)
+    graph = fn(Q, K, V, return_graph=True)
+    L = torch.empty(B, Hq, N, dtype=torch.float32, device=dev)
+    fwd, out = prepare_attention(graph, Q, K, V, cos=cos, sin=sin, save_lse=L)
+    scale = D ** -0.5
+
+    def step():
+        fwd()
+        run_backward(graph, Q, K, V, out, L, dO, scale, cos=cos, sin=sin)
+    ms = _time_launch(step, steps, warmup)
+    flops = int(3.5 * causal_flops(B, Hq, N, D))
+    return {"workload": "config 5: causal GQA + RoPE(base 5e5) fwd+bwd bf16 "
+                        "B=1 N=4096 Hq=32 Hkv=8 D=128",
+            "ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+            "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+            "algorithmic_flop_per_step": flops}
+
+
+def copy_calibration(reps=5):
+    """A plain device copy of COPY_BYTES (an elementwise negation: reads and
+    writes COPY_BYTES each) whose FETCH_SIZE / WRITE_SIZE counter readings
+    scale the counters of the attention kernels to bytes."""
+    import torch
+    n = COPY_BYTES // 2
+    src = torch.ones(n, dtype=torch.float16, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration": {"kernel": "neg (elementwise)", "reps": reps,
+                                           "bytes_read": COPY_BYTES,
+                                           "bytes_written": COPY_BYTES}}), flush=True)
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary
+    (lines 'TRAFFIC <kernel> fetch_bytes=F write_bytes=W total_bytes=T')."""
+    for f in sorted((ROOT / "profiles").glob("hbm_traffic_*.txt")):
+        for line in f.read_text().splitlines():
+            if line.startswith("TRAFFIC ") and kernel in line:
+                m = re.search(r"total_bytes=(\d+)", line)
+                if m:
+                    return int(m.group(1)), f"profiles/{f.name}"
+    return None, None
 
 
 def cpu_baseline(tensors, budget_s=10.0, max_heads=48):
@@ -148,6 +266,27 @@ def cpu_baseline(tensors, budget_s=10.0, max_heads=48):
                       f"N={N}, D={D}), fp32 torch on CPU, {t_total:.2f} s"}, err
 
 
+def cpu_config1(iters=10, warm=3):
+    """Config 1 in full on the CPU oracle: GPT-2-small causal forward,
+    B=1 H=12 N=512 D=64, fp32, median of ``iters`` runs after ``warm``."""
+    import torch
+
+    import oracle as O
+    g = torch.Generator().manual_seed(0)
+    B, H, N, D = C1["B"], C1["H"], C1["N"], C1["D"]
+    Q, K, V = (torch.randn(B, H, N, D, generator=g) for _ in range(3))
+    times = []
+    for i in range(warm + iters):
+        t0 = time.perf_counter()
+        O.naive_attention(Q, K, V, causal=True)
+        if i >= warm:
+            times.append(time.perf_counter() - t0)
+    ms = statistics.median(times) * 1e3
+    return {"workload": "config 1: GPT-2-small causal fwd fp32 B=1 H=12 N=512 D=64 (CPU oracle)",
+            "ms": round(ms, 3), "tflops": round(causal_flops(B, H, N, D) / (ms * 1e-3) / 1e12, 6),
+            "cores": torch.get_num_threads()}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -156,23 +295,24 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-alibi", action="store_true")
+    ap.add_argument("--no-train", action="store_true",
+                    help="skip the fwd+bwd configs 4 and 5")
+    ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: the fused-attention kernels run on "
               "a single GPU and this build has no multi-GPU path; run with "
               "--gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
-    import torch
     t_wall = time.time()
     ms, tensors = bench_forward(args.steps, args.warmup, alibi=False)
     flops = causal_flops(**C2)
     tflops = flops / (ms * 1e-3) / 1e12
-    ms_alibi = tflops_alibi = None
-    if not args.no_alibi:
-        ms_alibi, _ = bench_forward(args.steps, args.warmup, alibi=True)
-        tflops_alibi = flops / (ms_alibi * 1e-3) / 1e12
-
+    traffic, traffic_src = load_traffic(FWD_KERNEL)
     line = {
         "metric": "fwd TFLOPS (causal+RoPE, N=4096) + decode HBM GB/s (Llama-3-8B GQA 32k)",
         "value": round(tflops, 3),
@@ -194,11 +334,15 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3),
                      "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
-                     "traffic": None,
-                     "kernel": "fwd_kernel<F16,64,CAUSAL,NONE,SOFTMAX,ROPE,4>",
-                     "algorithmic_flop_per_launch": flops},
+                     "traffic": traffic,
+                     "traffic_source": traffic_src,
+                     "kernel": FWD_KERNEL,
+                     "algorithmic_flop_per_launch": flops,
+                     "algorithmic_bytes_per_launch": 4 * C2["B"] * C2["H"] * C2["N"] * C2["D"] * 2},
     }
-    if ms_alibi is not None:
+    if not args.no_alibi:
+        ms_alibi, _ = bench_forward(args.steps, args.warmup, alibi=True)
+        tflops_alibi = flops / (ms_alibi * 1e-3) / 1e12
         line["alibi"] = {"ms": round(ms_alibi, 5), "tflops": round(tflops_alibi, 3),
                          "frac": round(tflops_alibi / PEAK_FP16_TFLOPS, 4)}
     if not args.no_decode:
@@ -210,9 +354,13 @@ def main():
                           "bound": "hbm", "peak": PEAK_HBM_GBS,
                           "frac": round(gbs / PEAK_HBM_GBS, 4),
                           "algorithmic_bytes_per_launch": nbytes}
+    if not args.no_train:
+        line["bigbird"] = bench_bigbird(max(args.steps // 2, 1), max(args.warmup // 2, 1))
+        line["train"] = bench_train(max(args.steps // 2, 1), max(args.warmup // 2, 1))
     if not args.no_cpu:
         cb, err = cpu_baseline(tensors)
         line["cpu_baseline"] = cb
+        line["cpu_config1"] = cpu_config1()
         line["parity_max_abs_vs_oracle"] = err
     line["wall_s"] = round(time.time() - t_wall, 1)
     print(json.dumps(line), flush=True)
