@@ -105,7 +105,10 @@ def bench_forward(steps, warmup, alibi: bool):
     else:
         fn = af.attention(lambda Q, K, V: af.softmax(af.causal(af.rope(Q, K))) @ V)
     graph = fn(Q, K, V, return_graph=True)
-    launch, out = prepare_attention(graph, Q, K, V, cos=cos, sin=sin)
+    # config 2's slopes as written: 2^(-8(h+1)/H)
+    slopes = (torch.tensor([2.0 ** (-8.0 * (h + 1) / H) for h in range(H)],
+                           dtype=torch.float32, device=dev) if alibi else None)
+    launch, out = prepare_attention(graph, Q, K, V, cos=cos, sin=sin, alibi_slopes=slopes)
     ms = _time_launch(launch, steps, warmup)
     return ms, (Q, K, V, cos, sin, out)
 
@@ -331,6 +334,9 @@ def main():
                    "global_batch": C2["B"], "seq_len": C2["N"],
                    "heads": C2["H"], "head_dim": C2["D"],
                    "parallelism": "single GPU"},
+        # the reference's dense convention 4*B*H*N^2*D (rope_bench.py), for
+        # comparison with its published figures only
+        "dense_conv_tflops": round(4 * C2["B"] * C2["H"] * C2["N"] ** 2 * C2["D"] / (ms * 1e-3) / 1e12, 3),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3),
                      "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
@@ -344,7 +350,8 @@ def main():
         ms_alibi, _ = bench_forward(args.steps, args.warmup, alibi=True)
         tflops_alibi = flops / (ms_alibi * 1e-3) / 1e12
         line["alibi"] = {"ms": round(ms_alibi, 5), "tflops": round(tflops_alibi, 3),
-                         "frac": round(tflops_alibi / PEAK_FP16_TFLOPS, 4)}
+                         "frac": round(tflops_alibi / PEAK_FP16_TFLOPS, 4),
+                         "slopes": "2^(-8(h+1)/H), h=0..11 (config 2 as written)"}
     if not args.no_decode:
         ms_dec = bench_decode(args.steps, args.warmup)
         nbytes = decode_bytes(**{k: C3[k] for k in ("B", "Hq", "Hkv", "N", "D")})

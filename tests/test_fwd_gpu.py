@@ -256,3 +256,58 @@ def test_smoke_dense_matches_reference_test():
     Q = torch.randn(1, 2, 64, 32, device="cuda", dtype=torch.float16)
     out = fn(Q, torch.randn_like(Q), torch.randn_like(Q))
     assert out.shape == Q.shape and torch.isfinite(out).all()
+
+
+def _allowed(mask, Nq, Nkv, W):
+    """Closed-form keep sets (Nq x Nkv bool), independent of the kernels."""
+    i = torch.arange(Nq)[:, None]
+    j = torch.arange(Nkv)[None, :]
+    if mask == "dense":
+        return torch.ones(Nq, Nkv, dtype=torch.bool)
+    if mask == "causal":
+        return j <= i
+    if mask == "sw":
+        return (i - j).abs() < W
+    if mask == "sw_causal":
+        return (j <= i) & (i - j < W)
+    raise ValueError(mask)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("mask,Nq,Nkv", [("dense", 300, 300), ("dense", 77, 513),
+                                         ("causal", 512, 512), ("causal", 333, 333),
+                                         ("sw", 512, 512), ("sw_causal", 512, 512),
+                                         ("sw_causal", 301, 301), ("blocksparse", 512, 512)])
+def test_element_mask_exact(mask, Nq, Nkv, dtype):
+    """Q = 0 makes every allowed score 0, so P is uniform over the row's keep
+    set: the LSE is ln(count) (the count must come back exactly) and column 0
+    of O, with V[j, 0] = j / 512, is the mean kept key index.  Dropping,
+    adding or shifting any boundary key changes the count or moves the mean
+    by >= 1/512 (fp16 resolves it; bf16 checks the count only)."""
+    B, H, D, W = 1, 2, 64, 48
+    Q = torch.zeros(B, H, Nq, D, device="cuda", dtype=dtype)
+    K = torch.randn(B, H, Nkv, D, device="cuda", dtype=dtype)
+    V = torch.zeros(B, H, Nkv, D, device="cuda", dtype=dtype)
+    V[..., 0] = (torch.arange(Nkv, device="cuda") / 512).to(dtype)
+    L = torch.empty(B, H, Nq, dtype=torch.float32, device="cuda")
+    if mask == "blocksparse":
+        from attnfuse.runtime.block_mask import block_mask_from_blocks, run_block_sparse
+        nb = -(-Nq // 64)
+        grid = torch.zeros(nb, nb, dtype=torch.bool)
+        for a in range(nb):
+            grid[a, [0, a, max(a - 1, 0), (3 * a + 5) % nb]] = True
+        grid[0, :] = True
+        allowed = O.element_mask_from_grid(grid, Nq, Nkv, 64, 64)
+        out = run_block_sparse(Q, K, V, block_mask_from_blocks(grid, 64, 64, device="cuda"),
+                               D ** -0.5, save_lse=L)
+    else:
+        allowed = _allowed(mask, Nq, Nkv, W)
+        g = af.attention(variant(mask, H, window=W))(Q, K, V, return_graph=True)
+        out = run_attention(g, Q, K, V, save_lse=L)
+    torch.cuda.synchronize()
+    count = allowed.sum(1).double()
+    got_count = torch.exp(L.double().cpu()).round()
+    assert torch.equal(got_count, count.expand_as(got_count))
+    if dtype == torch.float16:
+        mean = (allowed.double() @ V[0, 0, :, 0].double().cpu()) / count
+        assert (out[..., 0].double().cpu() - mean).abs().max().item() <= 1e-3
