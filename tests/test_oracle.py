@@ -42,6 +42,12 @@ def _run_case(case, **override):
         args["scale"] = kw["scale"]
     if kw.get("q_offset"):
         args["query_offset"] = kw["q_offset"]
+    if kw.get("strict_causal"):
+        # planted off-by-one: the diagonal key hidden from its own query
+        args.pop("causal", None)
+        i = torch.arange(Q.shape[2])[:, None]
+        j = torch.arange(K.shape[2])[None, :]
+        args["elem_mask"] = j < i
     if kw.get("rope_base") is not None:
         n = max(Q.shape[2] + kw.get("q_offset", 0), K.shape[2])
         args["rope"] = O.rope_tables(n, Q.shape[-1], kw["rope_base"], torch.float64)
@@ -60,7 +66,8 @@ def test_oracle_matches_bruteforce_golden(case):
     assert torch.allclose(lse, want, atol=tol, rtol=0, equal_nan=False)
 
 
-@pytest.mark.parametrize("mutation", ["scale", "swap_kv", "drop_mask", "alibi_sign"])
+@pytest.mark.parametrize("mutation", ["scale", "swap_kv", "drop_mask", "alibi_sign",
+                                      "causal_off_by_one", "drop_rope"])
 def test_golden_catches_planted_mistakes(mutation):
     """A plausible oracle bug must make at least one golden case fail."""
     caught = False
@@ -75,8 +82,12 @@ def test_golden_catches_planted_mistakes(mutation):
             kw["window"] = None
         elif mutation == "alibi_sign" and case["kwargs"].get("slopes"):
             kw["slopes"] = [-s for s in case["kwargs"]["slopes"]]
+        elif mutation == "causal_off_by_one" and case["kwargs"].get("causal"):
+            kw["strict_causal"] = True
+        elif mutation == "drop_rope" and case["kwargs"].get("rope_base") is not None:
+            kw["rope_base"] = None
         out, _ = _run_case(case, **kw)
-        if not torch.allclose(out, _t(case["O"]), atol=1e-6):
+        if not torch.allclose(out, _t(case["O"]), atol=1e-6, equal_nan=False):
             caught = True
     assert caught
 
@@ -260,3 +271,27 @@ def test_expected_coverage_causal_staircase():
     for a in range(8):
         for b in range(4):
             assert cov[a, b] == int(64 * b <= 32 * a + 31)
+
+
+@pytest.mark.parametrize("Nq,Nkv,window", [(256, 256, 48), (333, 333, 7), (200, 200, 100),
+                                           (64, 300, 1)])
+def test_expected_coverage_is_any_visible_pair(Nq, Nkv, window):
+    """Every tile formula against brute force: a 32x64 tile is visited iff
+    some (i, j) pair inside it is visible under the element-level mask."""
+    i = torch.arange(Nq)[:, None]
+    j = torch.arange(Nkv)[None, :]
+    preds = {"full": torch.ones(Nq, Nkv, dtype=torch.bool),
+             "sliding_window": (i - j).abs() < window}
+    if Nq == Nkv:
+        preds["causal"] = j <= i
+        preds["causal_sliding_window"] = (j <= i) & (i - j < window)
+    g = torch.Generator().manual_seed(Nq)
+    grid = torch.rand(-(-Nq // 64), -(-Nkv // 128), generator=g) < 0.4
+    preds["block_sparse"] = O.element_mask_from_grid(grid, Nq, Nkv, 64, 128)
+    nq, nk = -(-Nq // 32), -(-Nkv // 64)
+    for mask, keep in preds.items():
+        pad = torch.zeros(nq * 32, nk * 64, dtype=torch.bool)
+        pad[:Nq, :Nkv] = keep
+        brute = pad.view(nq, 32, nk, 64).any(3).any(1).to(torch.int32)
+        got = O.expected_coverage(Nq, Nkv, mask=mask, window=window, grid=grid, bm=64, bn=128)
+        assert torch.equal(got, brute), mask
