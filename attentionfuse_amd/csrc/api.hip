@@ -52,10 +52,10 @@ int check_key(const af_spec_key& k, bool allow_bs) {
 int check_fwd_common(const af_fwd_args* a) {
   if (a == nullptr) return fail(AF_ERR_BAD_ARG, "args is NULL");
   int rc;
-  if ((rc = check_bhnd("q", a->q, a->q_stride))) return rc;
-  if ((rc = check_bhnd("k", a->k, a->k_stride))) return rc;
-  if ((rc = check_bhnd("v", a->v, a->v_stride))) return rc;
-  if ((rc = check_bhnd("o", a->o, a->o_stride))) return rc;
+  if ((rc = check_bhnd("q", a->q, a->q_stride, a->seqlen_q))) return rc;
+  if ((rc = check_bhnd("k", a->k, a->k_stride, a->seqlen_kv))) return rc;
+  if ((rc = check_bhnd("v", a->v, a->v_stride, a->seqlen_kv))) return rc;
+  if ((rc = check_bhnd("o", a->o, a->o_stride, a->seqlen_q))) return rc;
   if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seqlen_q < 0 || a->seqlen_kv < 0)
     return fail(AF_ERR_BAD_ARG, "bad sizes B=%d Hq=%d Hkv=%d Nq=%d Nkv=%d", a->batch, a->heads_q,
                 a->heads_kv, a->seqlen_q, a->seqlen_kv);
@@ -131,6 +131,11 @@ bool slice_fits_u32(int64_t rows, int64_t row_stride, int d) {
   return rows <= 0 || ((rows - 1) * row_stride + d) * 2 < (int64_t(1) << 32);
 }
 
+// Waves (32 query rows each) per forward workgroup for dense / causal /
+// windowed masks.  Measured on MI355X at D = 64: 8-wave workgroups (one per
+// CU) lose to two 4-wave workgroups per CU, whose barriers do not line up.
+int fwd_waves(const af_spec_key&) { return 4; }
+
 int dispatch_fwd(const FwdParams& p, const af_spec_key& k, int waves, hipStream_t s) {
   if (!slice_fits_u32(p.Nkv, p.ks[2], k.head_dim) || !slice_fits_u32(p.Nkv, p.vs[2], k.head_dim) ||
       (k.rope && !slice_fits_u32(p.rope_len, p.rs[0], k.head_dim)))
@@ -180,7 +185,7 @@ int af_fwd_tile(const af_spec_key* key, int32_t* block_m, int32_t* block_n) {
   if (key == nullptr) return fail(AF_ERR_BAD_ARG, "key is NULL");
   int rc = check_key(*key, true);
   if (rc) return rc;
-  if (block_m) *block_m = 128;
+  if (block_m) *block_m = 32 * fwd_waves(*key);
   if (block_n) *block_n = kKeysPerStage;
   return AF_OK;
 }
@@ -190,8 +195,9 @@ int af_fwd(const af_fwd_args* a, void* stream) {
   if (rc) return rc;
   if ((rc = check_key(a->key, false))) return rc;
   if (a->seqlen_q == 0) return AF_OK;
-  const FwdParams p = make_fwd_params(a, 128);
-  return dispatch_fwd(p, a->key, 4, static_cast<hipStream_t>(stream));
+  const int waves = fwd_waves(a->key);
+  const FwdParams p = make_fwd_params(a, 32 * waves);
+  return dispatch_fwd(p, a->key, waves, static_cast<hipStream_t>(stream));
 }
 
 int af_fwd_blocksparse(const af_fwd_args* a, const af_blockmask* bm, void* stream) {
@@ -244,9 +250,9 @@ size_t af_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t head_di
 int af_decode(const af_decode_args* a, void* workspace, size_t workspace_bytes, void* stream) {
   if (a == nullptr) return fail(AF_ERR_BAD_ARG, "args is NULL");
   int rc;
-  if ((rc = check_bhnd("q", a->q, a->q_stride))) return rc;
-  if ((rc = check_bhnd("k", a->k, a->k_stride))) return rc;
-  if ((rc = check_bhnd("v", a->v, a->v_stride))) return rc;
+  if ((rc = check_bhnd("q", a->q, a->q_stride, 1))) return rc;
+  if ((rc = check_bhnd("k", a->k, a->k_stride, a->seqlen_kv))) return rc;
+  if ((rc = check_bhnd("v", a->v, a->v_stride, a->seqlen_kv))) return rc;
   if (a->o == nullptr) return fail(AF_ERR_BAD_ARG, "o is NULL");
   if (a->o_stride[3] != 1) return fail(AF_ERR_BAD_ARG, "o: head-dim stride must be 1");
   if ((rc = check_key(a->key, false))) return rc;

@@ -36,9 +36,12 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   const void* ptrs[8] = {a->q, a->k, a->v, a->o, a->dout, a->dq, a->dk, a->dv};
   const int64_t* strides[8] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride,
                                a->do_stride, a->dq_stride, a->dk_stride, a->dv_stride};
+  // q, o, dout, dq have seqlen_q rows; k, v, dk, dv seqlen_kv
+  const int64_t nrows[8] = {a->seqlen_q, a->seqlen_kv, a->seqlen_kv, a->seqlen_q,
+                            a->seqlen_q,  a->seqlen_q,  a->seqlen_kv, a->seqlen_kv};
   for (int i = 0; i < 8; ++i)
-    if ((rc = check_bhnd(names[i], ptrs[i], strides[i]))) return rc;
-  if (a->lse == nullptr) return bad(AF_ERR_BAD_ARG, "lse is NULL");
+    if ((rc = check_bhnd(names[i], ptrs[i], strides[i], nrows[i]))) return rc;
+  if (a->lse == nullptr && a->seqlen_q > 0) return bad(AF_ERR_BAD_ARG, "lse is NULL");
   if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seqlen_q < 0 || a->seqlen_kv < 0 ||
       a->heads_q % a->heads_kv != 0)
     return bad(AF_ERR_BAD_ARG, "bad sizes (or query heads not a multiple of key/value heads)");
@@ -55,7 +58,7 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   }
   if (k.bias == AF_BIAS_ALIBI && a->alibi_slopes == nullptr) return bad(AF_ERR_BAD_ARG, "ALiBi needs slopes");
   const size_t need = bwd_workspace_bytes(a->batch, a->heads_q, a->seqlen_q);
-  if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
     return bad(AF_ERR_WORKSPACE, "backward workspace too small (af_bwd_workspace_bytes)");
 
   BwdParams p;

@@ -259,6 +259,10 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
   // key block outermost: under a causal mask the first key blocks see the
   // most query tiles, so they are dispatched first.
+  // no keys: nothing to write (the launch still has one workgroup)
+  if (p.n_kblocks <= 0) return;
+  // key block outermost: under a causal mask the first key blocks see the
+  // most query tiles, so they are dispatched first.
   const int BHK = p.B * p.Hkv;
   const int kb = blockIdx.x / BHK;
   const int bhk = blockIdx.x % BHK;
@@ -450,6 +454,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
+  // no queries: nothing to write (the launch still has one workgroup)
+  if (p.n_qblocks <= 0) return;
   const int BH = p.B * p.Hq;
   const int bh = blockIdx.x % BH;
   const int mbi = blockIdx.x / BH;

@@ -69,8 +69,10 @@ constexpr int v_pitch() {
   return D == 32 ? 32 : D + 32;
 }
 
+// Head dims up to 64 fit in 168 VGPRs (a few setup values spill outside the
+// loop): three waves per SIMD, three 4-wave workgroups per CU.
 template <class E, int D, int MASK, int BIAS, int NORM, bool ROPE, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64)
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 1)))
     fwd_kernel(const FwdParams p) {
   constexpr int NT = WAVES * 64;
   constexpr int BM = 32 * WAVES;
@@ -96,6 +98,9 @@ __global__ void __launch_bounds__(WAVES * 64)
   const int c = lane & 31;
 
   const int BH = p.B * p.Hq;
+  // m-block-major order: the heaviest query blocks of every head first.
+  // Workgroup g runs on XCD g % 8, so when B*H is a multiple of 8 each XCD
+  // works on a fixed eighth of the heads, whose K/V stay in its L2.
   const int bh = blockIdx.x % BH;
   const int mbi = blockIdx.x / BH;
   const bool heavy_last = MASK == MASK_CAUSAL || MASK == MASK_CSW;

@@ -77,8 +77,16 @@ def test_argument_errors_need_no_gpu():
     lib = N.lib()
     a = N.FwdArgsC()
     a.key = N.SpecKeyC(0, 64, 1, 0, 0, 0)
+    a.batch, a.heads_q, a.heads_kv, a.seqlen_q, a.seqlen_kv = 1, 4, 4, 64, 64
+    for s in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
+        s[:] = (64 * 4 * 64, 64 * 64, 64, 1)
     assert lib.af_fwd(a, None) == N.AF_ERR_BAD_ARG
     assert "NULL" in N.last_error()
+    # tensors with no rows are never touched and may be NULL: an empty
+    # problem is accepted and returns before any launch
+    a.seqlen_q = a.seqlen_kv = 0
+    assert lib.af_fwd(a, None) == N.AF_OK
+    a.seqlen_q = a.seqlen_kv = 64
     assert lib.af_fwd(None, None) == N.AF_ERR_BAD_ARG
     # misaligned / non-unit strides are refused before any launch
     a.q = a.k = a.v = a.o = 16

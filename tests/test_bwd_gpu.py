@@ -133,3 +133,25 @@ def test_backward_deterministic():
     torch.cuda.synchronize()
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("Nq,Nkv", [(64, 0), (0, 64), (1, 0)])
+def test_backward_with_an_empty_side(Nq, Nkv):
+    """No keys: O = 0 and dQ = 0; no queries: dK = dV = 0 (closed forms).
+    The tensors are slices of real allocations, so the kernels see valid
+    pointers with a zero length."""
+    g = torch.Generator(device="cuda").manual_seed(5)
+    base = {n: torch.randn(1, 2, 64, 64, generator=g, device="cuda", dtype=torch.float16)
+            for n in ("q", "k", "v", "do")}
+    q = base["q"][:, :, :Nq].clone().requires_grad_(True)
+    k = base["k"][:, :, :Nkv].clone().requires_grad_(True)
+    v = base["v"][:, :, :Nkv].clone().requires_grad_(True)
+    out = _fn("dense", 2)(q, k, v)
+    out.backward(base["do"][:, :, :Nq])
+    torch.cuda.synchronize()
+    assert out.shape == (1, 2, Nq, 64)
+    if Nkv == 0:
+        assert torch.count_nonzero(out) == 0
+    for t in (q, k, v):
+        assert t.grad is not None and t.grad.shape == t.shape
+        assert torch.count_nonzero(t.grad) == 0
