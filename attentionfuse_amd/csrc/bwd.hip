@@ -57,6 +57,15 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
     if (a->rope_len < std::max(a->seqlen_q, a->seqlen_kv)) return bad(AF_ERR_BAD_ARG, "rope tables too short");
   }
   if (k.bias == AF_BIAS_ALIBI && a->alibi_slopes == nullptr) return bad(AF_ERR_BAD_ARG, "ALiBi needs slopes");
+  // the kernels stage Q, dO, K, V and the RoPE tables through buffer
+  // resources with a 32-bit byte range per (batch, head) slice
+  auto fits = [&](int64_t rows, int64_t stride) {
+    return rows <= 0 || ((rows - 1) * stride + k.head_dim) * 2 < (int64_t(1) << 32);
+  };
+  if (!fits(a->seqlen_q, a->q_stride[2]) || !fits(a->seqlen_q, a->do_stride[2]) ||
+      !fits(a->seqlen_kv, a->k_stride[2]) || !fits(a->seqlen_kv, a->v_stride[2]) ||
+      (k.rope && !fits(a->rope_len, a->rope_stride[0])))
+    return bad(AF_ERR_UNSUPPORTED, "a (batch, head) slice spans 4 GiB or more");
   const size_t need = bwd_workspace_bytes(a->batch, a->heads_q, a->seqlen_q);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
     return bad(AF_ERR_WORKSPACE, "backward workspace too small (af_bwd_workspace_bytes)");
@@ -96,6 +105,7 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   p.Nkv = a->seqlen_kv;
   p.G = a->heads_q / a->heads_kv;
   p.window = a->window;
+  p.rope_len = a->rope_len;
   p.scale = a->scale;
 
   BwdGrids g;

@@ -60,6 +60,7 @@ struct BwdParams {
   int32_t B, Hq, Hkv, Nq, Nkv, G, window;
   int32_t bs_block_m, bs_block_n;
   int32_t n_qblocks, n_kblocks;   // workgroup tiling of the two kernels
+  int32_t rope_len;               // rows of the RoPE tables
   float scale;
 };
 
@@ -105,24 +106,24 @@ struct Tile32 {
   u32x4 cs[ROPE ? 2 : 1][2], sn[ROPE ? 2 : 1][2];
   int unit = -1;
 
-  __device__ void load(int u, const uint16_t* base, int64_t rstride, int r0, int nvalid,
-                       const uint16_t* cos, const uint16_t* sin, int64_t cstride) {
+  // Rows past the end of the tensor (or of the RoPE tables) fall outside the
+  // buffer resource and load as zeros.
+  __device__ void load(int u, __amdgpu_buffer_rsrc_t xr, int64_t rstride, int r0,
+                       __amdgpu_buffer_rsrc_t cr, __amdgpu_buffer_rsrc_t sr, int64_t cstride) {
     unit = u;
     const int rp = u / (D / 16), j = u % (D / 16);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int row = r0 + 2 * rp + t;
-      const bool ok = row >= 0 && row < nvalid;
-      const uint16_t* src = base + row * rstride + 8 * j;
-      x[t][0] = ok ? ld16(src) : u32x4{0, 0, 0, 0};
-      x[t][1] = ok ? ld16(src + D / 2) : u32x4{0, 0, 0, 0};
+      const uint32_t off = (uint32_t)((row * rstride + 8 * j) * 2);
+      x[t][0] = buf_ld16(xr, off);
+      x[t][1] = buf_ld16(xr, off + D);
       if constexpr (ROPE) {
-        const uint16_t* cp = cos + row * cstride + 8 * j;
-        const uint16_t* sp = sin + row * cstride + 8 * j;
-        cs[t][0] = ok ? ld16(cp) : u32x4{0, 0, 0, 0};
-        cs[t][1] = ok ? ld16(cp + D / 2) : u32x4{0, 0, 0, 0};
-        sn[t][0] = ok ? ld16(sp) : u32x4{0, 0, 0, 0};
-        sn[t][1] = ok ? ld16(sp + D / 2) : u32x4{0, 0, 0, 0};
+        const uint32_t co = (uint32_t)((row * cstride + 8 * j) * 2);
+        cs[t][0] = buf_ld16(cr, co);
+        cs[t][1] = buf_ld16(cr, co + D);
+        sn[t][0] = buf_ld16(sr, co);
+        sn[t][1] = buf_ld16(sr, co + D);
       }
     }
   }
@@ -240,6 +241,12 @@ __device__ __forceinline__ bool visible(int i, int j, int Nq, int Nkv, int W) {
   return ok;
 }
 
+// Byte range of `rows` rows of D elements at `rstride` elements apart.
+template <int D>
+__device__ __forceinline__ uint32_t span_bytes(int rows, int64_t rstride) {
+  return rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * rstride + D) * 2) : 0u;
+}
+
 // ---------------------------------------------------------------------------
 // dK / dV
 // ---------------------------------------------------------------------------
@@ -312,16 +319,21 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   QT qt[UPT];
   OT ot[UPT];
   float lreg = 0.f, dreg = 0.f;
+  const uint32_t rope_bytes = ROPE ? span_bytes<D>(p.rope_len, p.rs[0]) : 0u;
+  const auto crs = make_rsrc(p.cos, rope_bytes);
+  const auto srs = make_rsrc(p.sin, rope_bytes);
   auto stage_load = [&](int t) {
     const int gi = t / ntq, hq = hk * p.G + gi;
     const int m0 = tile_m0(t - gi * ntq);
+    const auto qrs = make_rsrc(p.q + b * p.qs[0] + hq * p.qs[1], span_bytes<D>(p.Nq, p.qs[2]));
+    const auto ors = make_rsrc(p.dout + b * p.dos[0] + hq * p.dos[1], span_bytes<D>(p.Nq, p.dos[2]));
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
       const int u = tid + i * NT;
       if (u < QT::UNITS)
-        qt[i].load(u, p.q + b * p.qs[0] + hq * p.qs[1], p.qs[2], m0, p.Nq, p.cos, p.sin, p.rs[0]);
+        qt[i].load(u, qrs, p.qs[2], m0, crs, srs, p.rs[0]);
       else if (u < 2 * QT::UNITS)
-        ot[i].load(u - QT::UNITS, p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], m0, p.Nq, nullptr, nullptr, 0);
+        ot[i].load(u - QT::UNITS, ors, p.dos[2], m0, crs, srs, 0);
     }
     if (tid < 32) {
       const int row = m0 + tid;
@@ -352,6 +364,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
     dv[db] = f32x16{};
   }
   const float c2 = p.scale * kLog2e;
+  constexpr bool kAlibiOneSided = BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW);
 
   if (ntiles > 0) {
     stage_load(0);
@@ -387,7 +400,40 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
       }
       float slope2 = 0.f;
       if constexpr (BIAS == BIAS_ALIBI) slope2 = p.slopes[hq] * kLog2e;
-      const bool need_mask = (MASK != MASK_FULL && MASK != MASK_BS) || m0 + 32 > p.Nq || n0w + 32 > p.Nkv;
+      // only tiles that cross the diagonal / window edge or run past an
+      // end need the per-element test
+      bool need_mask = m0 + 32 > p.Nq || n0w + 32 > p.Nkv;
+      if constexpr (MASK == MASK_CAUSAL) need_mask = need_mask || n0w + 31 > m0;
+      if constexpr (MASK == MASK_SW)
+        need_mask = need_mask || m0 + 31 - n0w >= p.window || n0w + 31 - m0 >= p.window;
+      if constexpr (MASK == MASK_CSW) need_mask = need_mask || n0w + 31 > m0 || m0 + 31 - n0w >= p.window;
+      // logits in log2 units: register r holds query m0 + 16 (r/8) + 8h + r%8
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        // causal-type masks see only j <= i, where -slope |i - j| is linear
+        // in the query index (one add per element)
+        float abias = 0.f;
+        if constexpr (kAlibiOneSided) abias = slope2 * (float)(key - (m0 + 16 * j + 8 * h));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int r = 8 * j + e;
+          float x = s[r] * c2;
+          if constexpr (kAlibiOneSided) {
+            x += abias;
+            abias -= slope2;
+          } else if constexpr (BIAS == BIAS_ALIBI) {
+            x -= slope2 * (float)abs(m0 + 16 * j + 8 * h + e - key);
+          }
+          s[r] = x;
+        }
+      }
+      if (need_mask) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qi = m0 + 16 * (r >> 3) + 8 * h + (r & 7);
+          s[r] = visible<MASK>(qi, key, p.Nq, p.Nkv, p.window) ? s[r] : -INFINITY;
+        }
+      }
       u32x4 pp[2], pd[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -399,13 +445,9 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int r = 8 * j + e;
-          const int qi = m0 + 16 * j + 8 * h + e;
-          float x = s[r] * c2;
-          if constexpr (BIAS == BIAS_ALIBI) x -= slope2 * (float)abs(qi - key);
           const float L2 = e < 4 ? l4a[e] : l4b[e - 4];
           const float dl = e < 4 ? d4a[e] : d4b[e - 4];
-          if (need_mask && !visible<MASK>(qi, key, p.Nq, p.Nkv, p.window)) x = -INFINITY;
-          const float pr = __builtin_amdgcn_exp2f(x - L2);
+          const float pr = __builtin_amdgcn_exp2f(s[r] - L2);
           pv[e] = pr;
           dsv[e] = pr * (dp[r] - dl);
         }
@@ -512,15 +554,20 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   const uint16_t* vbase = p.v + b * p.vs[0] + hk * p.vs[1];
   KT kt[UPT];
   VT vt[UPT];
+  const auto krs = make_rsrc(kbase, span_bytes<D>(p.Nkv, p.ks[2]));
+  const auto vrs = make_rsrc(vbase, span_bytes<D>(p.Nkv, p.vs[2]));
+  const uint32_t rope_bytes = ROPE ? span_bytes<D>(p.rope_len, p.rs[0]) : 0u;
+  const auto crs = make_rsrc(p.cos, rope_bytes);
+  const auto srs = make_rsrc(p.sin, rope_bytes);
   auto stage_load = [&](int t) {
     const int n0 = tile_n0(t);
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
       const int u = tid + i * NT;
       if (u < KT::UNITS)
-        kt[i].load(u, kbase, p.ks[2], n0, p.Nkv, p.cos, p.sin, p.rs[0]);
+        kt[i].load(u, krs, p.ks[2], n0, crs, srs, p.rs[0]);
       else if (u < 2 * KT::UNITS)
-        vt[i].load(u - KT::UNITS, vbase, p.vs[2], n0, p.Nkv, nullptr, nullptr, 0);
+        vt[i].load(u - KT::UNITS, vrs, p.vs[2], n0, crs, srs, 0);
     }
   };
   auto stage_store = [&](uint16_t* buf) {
@@ -538,6 +585,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   const float c2 = p.scale * kLog2e;
   float slope2 = 0.f;
   if constexpr (BIAS == BIAS_ALIBI) slope2 = p.slopes[hq] * kLog2e;
+  constexpr bool kAlibiOneSided = BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW);
 
   if (ntiles > 0) {
     stage_load(0);
@@ -566,7 +614,36 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
         s = E::mfma32(ld16(krow + 16 * ks), qf[ks], s);
         dp = E::mfma32(ld16(vrow + 16 * ks), of[ks], dp);
       }
-      const bool need_mask = (MASK != MASK_FULL && MASK != MASK_BS) || q0w + 32 > p.Nq || n0 + 32 > p.Nkv;
+      bool need_mask = q0w + 32 > p.Nq || n0 + 32 > p.Nkv;
+      if constexpr (MASK == MASK_CAUSAL) need_mask = need_mask || n0 + 31 > q0w;
+      if constexpr (MASK == MASK_SW)
+        need_mask = need_mask || q0w + 31 - n0 >= p.window || n0 + 31 - q0w >= p.window;
+      if constexpr (MASK == MASK_CSW) need_mask = need_mask || n0 + 31 > q0w || q0w + 31 - n0 >= p.window;
+      // logits in log2 units: register r holds key n0 + 16 (r/8) + 8h + r%8
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float abias = 0.f;
+        if constexpr (kAlibiOneSided) abias = slope2 * (float)(n0 + 16 * j + 8 * h - qrow);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int r = 8 * j + e;
+          float x = s[r] * c2;
+          if constexpr (kAlibiOneSided) {
+            x += abias;
+            abias += slope2;
+          } else if constexpr (BIAS == BIAS_ALIBI) {
+            x -= slope2 * (float)abs(qrow - (n0 + 16 * j + 8 * h + e));
+          }
+          s[r] = x;
+        }
+      }
+      if (need_mask) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kj = n0 + 16 * (r >> 3) + 8 * h + (r & 7);
+          s[r] = visible<MASK>(qrow, kj, p.Nq, p.Nkv, p.window) ? s[r] : -INFINITY;
+        }
+      }
       u32x4 pd[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -574,11 +651,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int r = 8 * j + e;
-          const int kj = n0 + 16 * j + 8 * h + e;
-          float x = s[r] * c2;
-          if constexpr (BIAS == BIAS_ALIBI) x -= slope2 * (float)abs(qrow - kj);
-          if (need_mask && !visible<MASK>(qrow, kj, p.Nq, p.Nkv, p.window)) x = -INFINITY;
-          const float pr = __builtin_amdgcn_exp2f(x - L2);
+          const float pr = __builtin_amdgcn_exp2f(s[r] - L2);
           dsv[e] = pr * (dp[r] - dl);
         }
 #pragma unroll
