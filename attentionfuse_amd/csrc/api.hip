@@ -308,8 +308,8 @@ int af_decode(const af_decode_args* a, void* workspace, size_t workspace_bytes, 
   return AF_OK;
 }
 
-size_t af_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q) {
-  return bwd_workspace_bytes(batch, heads_q, seqlen_q);
+size_t af_bwd_workspace_bytes(const af_bwd_args* args) {
+  return args == nullptr ? 0 : bwd_workspace_bytes(*args);
 }
 
 int af_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_t workspace_bytes,

@@ -10,10 +10,26 @@
 
 namespace af {
 
-size_t bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q) {
-  if (batch <= 0 || heads_q <= 0 || seqlen_q < 0) return 0;
-  return (size_t)batch * heads_q * seqlen_q * sizeof(float);
+BwdWorkspace bwd_workspace_layout(const af_bwd_args& a) {
+  auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
+  BwdWorkspace w{0, 0, 0, 0};
+  if (a.batch <= 0 || a.heads_q <= 0 || a.heads_kv <= 0 || a.seqlen_q < 0 || a.seqlen_kv < 0 || a.key.head_dim <= 0)
+    return w;
+  const size_t rows_q = (size_t)a.batch * a.heads_q * a.seqlen_q;
+  const size_t rows_k = (size_t)a.batch * a.heads_kv * a.seqlen_kv;
+  w.delta = 0;
+  w.total = up(rows_q * sizeof(float));
+  if (a.key.rope) {
+    w.qr = w.total;
+    w.total += up(rows_q * a.key.head_dim * 2);
+    w.kr = w.total;
+    w.total += up(rows_k * a.key.head_dim * 2);
+  }
+  if (rows_q == 0 && rows_k == 0) w.total = 0;
+  return w;
 }
+
+size_t bwd_workspace_bytes(const af_bwd_args& a) { return bwd_workspace_layout(a).total; }
 
 static int bad(int code, const char* msg) {
   set_error("%s", msg);
@@ -66,7 +82,8 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
       !fits(a->seqlen_kv, a->k_stride[2]) || !fits(a->seqlen_kv, a->v_stride[2]) ||
       (k.rope && !fits(a->rope_len, a->rope_stride[0])))
     return bad(AF_ERR_UNSUPPORTED, "a (batch, head) slice spans 4 GiB or more");
-  const size_t need = bwd_workspace_bytes(a->batch, a->heads_q, a->seqlen_q);
+  const BwdWorkspace wl = bwd_workspace_layout(*a);
+  const size_t need = wl.total;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
     return bad(AF_ERR_WORKSPACE, "backward workspace too small (af_bwd_workspace_bytes)");
 
@@ -78,7 +95,12 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   p.o = static_cast<const uint16_t*>(a->o);
   p.dout = static_cast<const uint16_t*>(a->dout);
   p.lse = a->lse;
-  p.delta = static_cast<float*>(workspace);
+  char* ws = static_cast<char*>(workspace);
+  p.delta = reinterpret_cast<float*>(ws + wl.delta);
+  if (k.rope) {
+    p.qr = reinterpret_cast<uint16_t*>(ws + wl.qr);
+    p.kr = reinterpret_cast<uint16_t*>(ws + wl.kr);
+  }
   p.dq = static_cast<uint16_t*>(a->dq);
   p.dk = static_cast<uint16_t*>(a->dk);
   p.dv = static_cast<uint16_t*>(a->dv);
@@ -107,6 +129,26 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   p.window = a->window;
   p.rope_len = a->rope_len;
   p.scale = a->scale;
+  // the score kernels read q~ / k~ from the rotated workspace copies (RoPE)
+  // or straight from the inputs
+  const int64_t D = k.head_dim;
+  if (k.rope) {
+    p.qt = p.qr;
+    p.kt = p.kr;
+    const int64_t qts[4] = {(int64_t)a->heads_q * a->seqlen_q * D, (int64_t)a->seqlen_q * D, D, 1};
+    const int64_t kts[4] = {(int64_t)a->heads_kv * a->seqlen_kv * D, (int64_t)a->seqlen_kv * D, D, 1};
+    for (int i = 0; i < 4; ++i) {
+      p.qts[i] = qts[i];
+      p.kts[i] = kts[i];
+    }
+  } else {
+    p.qt = p.q;
+    p.kt = p.k;
+    for (int i = 0; i < 4; ++i) {
+      p.qts[i] = p.qs[i];
+      p.kts[i] = p.ks[i];
+    }
+  }
 
   BwdGrids g;
   g.waves_kv = 4;
@@ -138,9 +180,10 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   const int BK = 32 * g.waves_kv, BMq = 32 * g.waves_q;
   p.n_kblocks = (a->seqlen_kv + BK - 1) / BK;
   p.n_qblocks = (a->seqlen_q + BMq - 1) / BMq;
-  const int64_t rows = (int64_t)a->batch * a->heads_q * a->seqlen_q;
-  const int rpb = 256 / (k.head_dim / 8);
-  g.delta = (unsigned)std::max<int64_t>(1, (rows + rpb - 1) / rpb);
+  const int64_t rows = (int64_t)a->batch * a->heads_q * a->seqlen_q +
+                       (k.rope ? (int64_t)a->batch * a->heads_kv * a->seqlen_kv : 0);
+  const int rpb = 256 / (k.head_dim / 16);
+  g.prep = (unsigned)std::max<int64_t>(1, (rows + rpb - 1) / rpb);
   g.dkv = (unsigned)std::max(1, p.n_kblocks * a->batch * a->heads_kv);
   g.dq = (unsigned)std::max(1, p.n_qblocks * a->batch * a->heads_q);
 

@@ -24,7 +24,7 @@ namespace {
 
 template <int MASK, int BIAS, bool ROPE, int WK, int WQ>
 void go(const BwdParams& p, const BwdGrids& g, hipStream_t s) {
-  hipLaunchKernelGGL((bwd_delta_kernel<Elem, AF_D>), dim3(g.delta), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((bwd_prep_kernel<Elem, AF_D, ROPE>), dim3(g.prep), dim3(256), 0, s, p);
   hipLaunchKernelGGL((bwd_dkv_kernel<Elem, AF_D, MASK, BIAS, ROPE, WK>), dim3(g.dkv), dim3(64 * WK), 0, s, p);
   hipLaunchKernelGGL((bwd_dq_kernel<Elem, AF_D, MASK, BIAS, ROPE, WQ>), dim3(g.dq), dim3(64 * WQ), 0, s, p);
 }

@@ -2,7 +2,7 @@
 // piece (d)).
 //
 // Math (FA2; reference: attnfuse/compiler/codegen_backward.py:45-302):
-//   delta_i = sum_d dO_id O_id                          (bwd_delta_kernel)
+//   delta_i = sum_d dO_id O_id
 //   P_ij    = exp(S_ij - L_i),  S = scale * q~ k~^T + bias,  masked -> 0
 //   dV_j    = sum_i P_ij dO_i
 //   dP_ij   = dO_i . v_j,   dS_ij = P_ij (dP_ij - delta_i)
@@ -15,19 +15,29 @@
 // attnfuse/runtime/backward.py:77-79).
 //
 // Decomposition:
+//  * bwd_prep_kernel: delta per query row, and with RoPE the rotated q~ and
+//    k~ written once to the workspace, rounded to the input dtype exactly as
+//    the forward rounds them in registers.  Every query tile is read by all
+//    key blocks (and every key tile by all query blocks), so rotating once
+//    replaces one rotation (and one cos/sin read) per visit.
 //  * bwd_dkv_kernel: a workgroup owns 32*WAVES keys of one (batch, kv head);
-//    each wave owns 32 keys with k~ and v held in registers as MFMA B
-//    operands.  It walks the query tiles (32 rows) of every query head of
-//    the GQA group, so dK/dV come out group-summed with no atomics.  Score
-//    tiles are S (queries x keys) with the query rows permuted (kperm) so
-//    that P and dS feed the dV^T and dK^T MFMAs straight from registers.
+//    each wave owns 32 keys, k~ in registers (and v too for D <= 64; for
+//    D = 128 the workgroup's V block sits in LDS so that the dK/dV
+//    accumulators, k~ and the score tiles fit two waves per SIMD).  It walks
+//    the 32-row query tiles of every query head of the GQA group, so dK/dV
+//    come out group-summed with no atomics.  Scores are S (queries x keys)
+//    with the query rows permuted (kperm), so P and dS feed the dV^T and dK^T
+//    MFMAs straight from registers.
 //  * bwd_dq_kernel: a workgroup owns 32*WAVES query rows of one (batch,
-//    head); q~ and dO stay in registers; key tiles (32 keys) stream through
-//    LDS as k~, k~^T and v.  Scores are S^T (keys x queries) so dS^T is the
-//    B operand of the dQ^T MFMA.
-//  * Both kernels stage 32-row tiles into LDS double-buffered (global loads
-//    of tile t+1 in flight during the MFMAs of tile t), writing rows and,
-//    where an MFMA needs the contraction index contiguous, the transpose.
+//    head); q~ and dO stay in registers; 32-key tiles of k~ and v stream
+//    through LDS.  Scores are S^T (keys x queries) so dS^T is the B operand of
+//    the dQ^T MFMA.
+//  * LDS tiles are row-major with no padding and an XOR swizzle of their
+//    16-byte chunks (lds_swz): the row reads of the score MFMAs and the
+//    transposing reads (ds_read_b64_tr_b16) of the gradient MFMAs both hit
+//    64 distinct banks, so no transposed copy of any tile is stored.
+//  * Tiles are double-buffered: buffer loads (rows past the end load as
+//    zeros) of tile t+1 are in flight while tile t is on the MFMA pipes.
 #pragma once
 
 #include "af_common.hpp"
@@ -43,6 +53,10 @@ struct BwdParams {
   const uint16_t* dout;
   const float* lse;
   float* delta;            // (B, Hq, Nq) fp32 workspace
+  uint16_t* qr;            // RoPE: q~ workspace, (B, Hq, Nq, D) contiguous
+  uint16_t* kr;            // RoPE: k~ workspace, (B, Hkv, Nkv, D) contiguous
+  const uint16_t* qt;      // q~ as the score kernels read it (qr, or q)
+  const uint16_t* kt;      // k~ likewise (kr, or k)
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
@@ -56,6 +70,7 @@ struct BwdParams {
   const int32_t* bs_q_num;
   const int32_t* bs_q_idx;
   int64_t qs[4], ks[4], vs[4], os[4], dos[4], dqs[4], dks[4], dvs[4], ls[3], rs[2];
+  int64_t qts[4], kts[4];  // strides of qt, kt
   int64_t bs_full_rs, bs_part_rs, bs_q_rs;
   int32_t B, Hq, Hkv, Nq, Nkv, G, window;
   int32_t bs_block_m, bs_block_n;
@@ -64,116 +79,113 @@ struct BwdParams {
   float scale;
 };
 
-// ---------------------------------------------------------------------------
-// delta = rowsum(dO * O), fp32.
-// ---------------------------------------------------------------------------
-template <class E, int D>
-__global__ void __launch_bounds__(256) bwd_delta_kernel(const BwdParams p) {
-  constexpr int CPR = D / 8;          // 16-byte chunks per row
-  constexpr int RPB = 256 / CPR;      // rows per workgroup
-  const int tid = threadIdx.x;
-  const int64_t r = (int64_t)blockIdx.x * RPB + tid / CPR;
-  const int ch = tid % CPR;
-  const int64_t total = (int64_t)p.B * p.Hq * p.Nq;
-  float acc = 0.f;
-  if (r < total) {
-    const int i = (int)(r % p.Nq);
-    const int64_t bh = r / p.Nq;
-    const int hq = (int)(bh % p.Hq), b = (int)(bh / p.Hq);
-    float fo[8], fd[8];
-    unpack8<E>(ld16(p.o + b * p.os[0] + hq * p.os[1] + i * p.os[2] + 8 * ch), fo);
-    unpack8<E>(ld16(p.dout + b * p.dos[0] + hq * p.dos[1] + i * p.dos[2] + 8 * ch), fd);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc += fo[e] * fd[e];
-  }
-#pragma unroll
-  for (int off = 1; off < CPR; off <<= 1) acc += __shfl_xor(acc, off, 64);
-  if (r < total && ch == 0) p.delta[r] = acc;
+// Byte range of `rows` rows of D elements at `rstride` elements apart.
+template <int D>
+__device__ __forceinline__ uint32_t span_bytes(int rows, int64_t rstride) {
+  return rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * rstride + D) * 2) : 0u;
 }
 
 // ---------------------------------------------------------------------------
-// 32-row tile staging.  A unit is (row pair rp, rotate-half pair j): rows
-// 2rp, 2rp+1 and the 16-byte chunks j and j + D/16 of each.  The tile is
-// written row-major (pitch D+8) and, when TRANS, transposed (pitch 40) as
-// packed (row 2rp, row 2rp+1) words.
+// LDS tile swizzle.  A tile row holds D elements = D/8 chunks of 16 bytes;
+// logical chunk k of row r is stored at chunk k ^ lds_swz<D>(r).  The
+// function depends on r mod 16 only, so tiles can be addressed at 16-row
+// offsets without re-swizzling.  Chosen so that (a) 16 lanes reading the
+// same chunk of 16 different rows (the MFMA row operands) and (b) the
+// 32-lane passes of ds_read_b64_tr_b16 (4 rows x 4 consecutive chunks) each
+// touch 64 distinct banks.
 // ---------------------------------------------------------------------------
-template <class E, int D, bool ROPE, bool TRANS>
-struct Tile32 {
-  static constexpr int UNITS = 16 * (D / 16);
-  static constexpr int RP = D + 8;     // row-major pitch
-  static constexpr int TP = 32 + 8;    // transposed pitch
-  u32x4 x[2][2];                        // [row][lo/hi]
-  u32x4 cs[ROPE ? 2 : 1][2], sn[ROPE ? 2 : 1][2];
-  int unit = -1;
+template <int D>
+__device__ __forceinline__ int lds_swz(int r) {
+  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else if constexpr (D == 64) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else return (r >> 2) & 3;
+}
+// element offset of element `col` of row `r`
+template <int D>
+__device__ __forceinline__ int lds_at(int r, int col) {
+  return r * D + 8 * ((col >> 3) ^ lds_swz<D>(r)) + (col & 7);
+}
+// Per-lane offset of the two ds_read_b64_tr_b16 (t = 0, 1) that together
+// give this lane the 32x32x16 A operand X^T[32 db + l%32][rows 8h .. 8h+7]
+// of the first 16 rows of a row-major, swizzled (rows x D) tile -- the
+// read pattern tr_source_offset describes for padded tiles.  Add 16*j*D
+// for rows 16j .. 16j+15.
+template <int D>
+__device__ __forceinline__ int tr_at(int lane, int t, int db) {
+  const int row = 8 * (lane >> 5) + 4 * t + ((lane & 15) >> 2);
+  const int col = 32 * db + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  return lds_at<D>(row, col);
+}
 
-  // Rows past the end of the tensor (or of the RoPE tables) fall outside the
-  // buffer resource and load as zeros.
-  __device__ void load(int u, __amdgpu_buffer_rsrc_t xr, int64_t rstride, int r0,
-                       __amdgpu_buffer_rsrc_t cr, __amdgpu_buffer_rsrc_t sr, int64_t cstride) {
-    unit = u;
-    const int rp = u / (D / 16), j = u % (D / 16);
+// ---------------------------------------------------------------------------
+// delta = rowsum(dO * O), fp32; with RoPE also q~ and k~ into the workspace.
+// A row is handled by D/16 threads, thread j holding the rotate-half pair of
+// chunks j and j + D/16.  Rows [0, B*Hq*Nq) are query rows, the next
+// B*Hkv*Nkv (RoPE only) key rows.
+// ---------------------------------------------------------------------------
+template <class E, int D, bool ROPE>
+__global__ void __launch_bounds__(256) bwd_prep_kernel(const BwdParams p) {
+  constexpr int TPR = D / 16;          // threads per row
+  constexpr int RPB = 256 / TPR;       // rows per workgroup
+  const int tid = threadIdx.x;
+  const int64_t r = (int64_t)blockIdx.x * RPB + tid / TPR;
+  const int j = tid % TPR;
+  const int64_t nq = (int64_t)p.B * p.Hq * p.Nq;
+  const int64_t nk = ROPE ? (int64_t)p.B * p.Hkv * p.Nkv : 0;
+  if (r < nq) {
+    const int i = (int)(r % p.Nq);
+    const int64_t bh = r / p.Nq;
+    const int hq = (int)(bh % p.Hq), b = (int)(bh / p.Hq);
+    const uint16_t* orow = p.o + b * p.os[0] + hq * p.os[1] + i * p.os[2];
+    const uint16_t* drow = p.dout + b * p.dos[0] + hq * p.dos[1] + i * p.dos[2];
+    float fo[8], fd[8], acc = 0.f;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int row = r0 + 2 * rp + t;
-      const uint32_t off = (uint32_t)((row * rstride + 8 * j) * 2);
-      x[t][0] = buf_ld16(xr, off);
-      x[t][1] = buf_ld16(xr, off + D);
-      if constexpr (ROPE) {
-        const uint32_t co = (uint32_t)((row * cstride + 8 * j) * 2);
-        cs[t][0] = buf_ld16(cr, co);
-        cs[t][1] = buf_ld16(cr, co + D);
-        sn[t][0] = buf_ld16(sr, co);
-        sn[t][1] = buf_ld16(sr, co + D);
-      }
+    for (int half = 0; half < 2; ++half) {
+      unpack8<E>(ld16(orow + 8 * j + half * (D / 2)), fo);
+      unpack8<E>(ld16(drow + 8 * j + half * (D / 2)), fd);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += fo[e] * fd[e];
     }
-  }
-
-  __device__ void store(uint16_t* rows, uint16_t* trans) {
-    const int rp = unit / (D / 16), j = unit % (D / 16);
+#pragma unroll
+    for (int off = 1; off < TPR; off <<= 1) acc += __shfl_xor(acc, off, 64);
+    if (j == 0) p.delta[r] = acc;
     if constexpr (ROPE) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) rope_pair<E>(x[t][0], x[t][1], cs[t][0], sn[t][0], cs[t][1], sn[t][1]);
+      const uint16_t* qrow = p.q + b * p.qs[0] + hq * p.qs[1] + i * p.qs[2];
+      const uint16_t* cr = p.cos + i * p.rs[0];
+      const uint16_t* sr = p.sin + i * p.rs[0];
+      const int dl = 8 * j, dh = dl + D / 2;
+      u32x4 lo = ld16(qrow + dl), hi = ld16(qrow + dh);
+      rope_pair<E>(lo, hi, ld16(cr + dl), ld16(sr + dl), ld16(cr + dh), ld16(sr + dh));
+      uint16_t* out = p.qr + r * D;
+      st16(out + dl, lo);
+      st16(out + dh, hi);
     }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      st16(rows + (2 * rp + t) * RP + 8 * j, x[t][0]);
-      st16(rows + (2 * rp + t) * RP + 8 * j + D / 2, x[t][1]);
-    }
-    if constexpr (TRANS) {
-      uint32_t* t32 = reinterpret_cast<uint32_t*>(trans);
-#pragma unroll
-      for (int half = 0; half < 2; ++half)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t a = x[0][half][e >> 1], bq = x[1][half][e >> 1];
-          const uint32_t word = (e & 1) ? ((a >> 16) | (bq & 0xffff0000u)) : ((a & 0xffffu) | (bq << 16));
-          const int d = 8 * j + half * (D / 2) + e;
-          t32[(d * TP + 2 * rp) >> 1] = word;
-        }
-    }
+  } else if (ROPE && r < nq + nk) {
+    const int64_t rk = r - nq;
+    const int n = (int)(rk % p.Nkv);
+    const int64_t bh = rk / p.Nkv;
+    const int hk = (int)(bh % p.Hkv), b = (int)(bh / p.Hkv);
+    const uint16_t* krow = p.k + b * p.ks[0] + hk * p.ks[1] + n * p.ks[2];
+    const uint16_t* cr = p.cos + n * p.rs[0];
+    const uint16_t* sr = p.sin + n * p.rs[0];
+    const int dl = 8 * j, dh = dl + D / 2;
+    u32x4 lo = ld16(krow + dl), hi = ld16(krow + dh);
+    rope_pair<E>(lo, hi, ld16(cr + dl), ld16(sr + dl), ld16(cr + dh), ld16(sr + dh));
+    uint16_t* out = p.kr + rk * D;
+    st16(out + dl, lo);
+    st16(out + dh, hi);
   }
-};
+}
 
 // Registers of a 32-row operand held by a wave: lane (h, c) holds row c,
-// dims 16 ks + 8 h .. +7, rotated when ROPE.
-template <class E, int D, bool ROPE>
+// dims 16 ks + 8 h .. +7 (rows past nvalid are zero).
+template <int D>
 __device__ inline void load_operand_rows(u32x4* f, const uint16_t* base, int64_t rstride, int row, int nvalid,
-                                         const uint16_t* cos, const uint16_t* sin, int64_t cstride, int h) {
+                                         int h) {
   constexpr int KS = D / 16;
   const bool ok = row < nvalid;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) f[ks] = ok ? ld16(base + row * rstride + 16 * ks + 8 * h) : u32x4{0, 0, 0, 0};
-  if constexpr (ROPE) {
-    if (ok) {
-      const uint16_t* cr = cos + row * cstride;
-      const uint16_t* sr = sin + row * cstride;
-#pragma unroll
-      for (int ks = 0; ks < KS / 2; ++ks) {
-        const int dl = 16 * ks + 8 * h, dh = dl + D / 2;
-        rope_pair<E>(f[ks], f[ks + KS / 2], ld16(cr + dl), ld16(sr + dl), ld16(cr + dh), ld16(sr + dh));
-      }
-    }
-  }
 }
 
 // Store a transposed 32x32-block gradient accumulator (rows = dims,
@@ -230,8 +242,8 @@ __device__ inline void store_grad_rows(f32x16* acc, uint16_t* out, int64_t rstri
     }
 }
 
-// Masking of one score element (query i, key j); the range logic of the
-// forward kernel decides which tiles are visited at all.
+// Masking of one score element (query i, key j); the range logic of each
+// kernel decides which tiles are visited at all and which need this test.
 template <int MASK>
 __device__ __forceinline__ bool visible(int i, int j, int Nq, int Nkv, int W) {
   bool ok = i < Nq && j < Nkv;
@@ -241,11 +253,40 @@ __device__ __forceinline__ bool visible(int i, int j, int Nq, int Nkv, int W) {
   return ok;
 }
 
-// Byte range of `rows` rows of D elements at `rstride` elements apart.
-template <int D>
-__device__ __forceinline__ uint32_t span_bytes(int rows, int64_t rstride) {
-  return rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * rstride + D) * 2) : 0u;
-}
+// Staging of two 32-row tiles (rows [r0, r0 + 32) of tensors A and B, D
+// elements each) through registers into one swizzled LDS stage: tile A at
+// buf, tile B at buf + 32 D.
+template <int D, int NT>
+struct TilePair {
+  static constexpr int CHUNKS = 32 * D / 8;               // per tensor
+  static constexpr int CPT = (2 * CHUNKS + NT - 1) / NT;  // per thread
+  u32x4 x[CPT];
+
+  __device__ void load(int tid, __amdgpu_buffer_rsrc_t ar, int64_t astride, __amdgpu_buffer_rsrc_t br,
+                       int64_t bstride, int r0) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int g = tid + i * NT;
+      if (2 * CHUNKS % NT != 0 && g >= 2 * CHUNKS) continue;
+      const int rem = g % CHUNKS;
+      const int row = rem / (D / 8), k = rem % (D / 8);
+      if (g < CHUNKS)
+        x[i] = buf_ld16(ar, (uint32_t)(((r0 + row) * astride + 8 * k) * 2));
+      else
+        x[i] = buf_ld16(br, (uint32_t)(((r0 + row) * bstride + 8 * k) * 2));
+    }
+  }
+  __device__ void store(int tid, uint16_t* buf) const {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int g = tid + i * NT;
+      if (2 * CHUNKS % NT != 0 && g >= 2 * CHUNKS) continue;
+      const int rem = g % CHUNKS;
+      const int row = rem / (D / 8), k = rem % (D / 8);
+      st16(buf + (g >= CHUNKS ? 32 * D : 0) + lds_at<D>(row, 8 * k), x[i]);
+    }
+  }
+};
 
 // ---------------------------------------------------------------------------
 // dK / dV
@@ -255,19 +296,15 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   constexpr int NT = WAVES * 64;
   constexpr int BK = 32 * WAVES;
   constexpr int KS = D / 16, DB = D / 32;
-  using QT = Tile32<E, D, ROPE, true>;
-  using OT = Tile32<E, D, false, true>;
-  constexpr int RP = QT::RP, TP = QT::TP;
-  constexpr int ROWS = 32 * RP, TRS = D * TP;
-  constexpr int STAGE = 2 * ROWS + 2 * TRS + 2 * 2 * 32;   // halves; 64 floats at the end
-  constexpr int UPT = (2 * QT::UNITS + NT - 1) / NT;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+  constexpr bool VLDS = D > 64;            // V block in LDS instead of registers
+  constexpr int TILE = 32 * D;             // one 32-row tile (elements)
+  constexpr int STAGE = 2 * TILE + 128;    // q~ tile, dO tile, 32 L + 32 delta floats
+  constexpr int VBLK = VLDS ? BK * D : 0;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE + VBLK];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
-  // key block outermost: under a causal mask the first key blocks see the
-  // most query tiles, so they are dispatched first.
   // no keys: nothing to write (the launch still has one workgroup)
   if (p.n_kblocks <= 0) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
   // key block outermost: under a causal mask the first key blocks see the
   // most query tiles, so they are dispatched first.
   const int BHK = p.B * p.Hkv;
@@ -278,12 +315,24 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   const int n0w = n0 + 32 * w;
   const int key = n0w + c;
 
-  // k~ and v for this wave's 32 keys, as B operands (lane: row c).
-  u32x4 kf[KS], vf[KS];
-  load_operand_rows<E, D, ROPE>(kf, p.k + b * p.ks[0] + hk * p.ks[1], p.ks[2], key, p.Nkv, p.cos, p.sin,
-                                p.rs[0], h);
-  load_operand_rows<E, D, false>(vf, p.v + b * p.vs[0] + hk * p.vs[1], p.vs[2], key, p.Nkv, nullptr, nullptr, 0,
-                                 h);
+  // k~ (and v) for this wave's 32 keys, as B operands (lane: row c).
+  u32x4 kf[KS], vf[VLDS ? 1 : KS];
+  load_operand_rows<D>(kf, p.kt + b * p.kts[0] + hk * p.kts[1], p.kts[2], key, p.Nkv, h);
+  const uint16_t* vbase = p.v + b * p.vs[0] + hk * p.vs[1];
+  uint16_t* const vblk = lds + 2 * STAGE;
+  if constexpr (VLDS) {
+    const auto vrs = make_rsrc(vbase, span_bytes<D>(p.Nkv, p.vs[2]));
+    // key row r is stored at block row kperm(r), so a wave's V operand reads
+    // use the same per-lane offsets as its (permuted) query-row reads
+    constexpr int VCH = BK * D / 8;
+#pragma unroll
+    for (int i = 0; i < VCH / NT; ++i) {
+      const int g = tid + i * NT, row = g / (D / 8), kc = g % (D / 8);
+      st16(vblk + lds_at<D>(kperm(row), 8 * kc), buf_ld16(vrs, (uint32_t)(((n0 + row) * p.vs[2] + 8 * kc) * 2)));
+    }
+  } else {
+    load_operand_rows<D>(vf, vbase, p.vs[2], key, p.Nkv, h);
+  }
 
   // query-tile schedule (tiles of 32 rows) for one head
   int m_lo = 0, m_hi = p.Nq, ntq;
@@ -316,45 +365,30 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   };
   const int ntiles = ntq * p.G;
 
-  QT qt[UPT];
-  OT ot[UPT];
+  TilePair<D, NT> st;
   float lreg = 0.f, dreg = 0.f;
-  const uint32_t rope_bytes = ROPE ? span_bytes<D>(p.rope_len, p.rs[0]) : 0u;
-  const auto crs = make_rsrc(p.cos, rope_bytes);
-  const auto srs = make_rsrc(p.sin, rope_bytes);
   auto stage_load = [&](int t) {
     const int gi = t / ntq, hq = hk * p.G + gi;
     const int m0 = tile_m0(t - gi * ntq);
-    const auto qrs = make_rsrc(p.q + b * p.qs[0] + hq * p.qs[1], span_bytes<D>(p.Nq, p.qs[2]));
+    const auto qrs = make_rsrc(p.qt + b * p.qts[0] + hq * p.qts[1], span_bytes<D>(p.Nq, p.qts[2]));
     const auto ors = make_rsrc(p.dout + b * p.dos[0] + hq * p.dos[1], span_bytes<D>(p.Nq, p.dos[2]));
-#pragma unroll
-    for (int i = 0; i < UPT; ++i) {
-      const int u = tid + i * NT;
-      if (u < QT::UNITS)
-        qt[i].load(u, qrs, p.qs[2], m0, crs, srs, p.rs[0]);
-      else if (u < 2 * QT::UNITS)
-        ot[i].load(u - QT::UNITS, ors, p.dos[2], m0, crs, srs, 0);
-    }
-    if (tid < 32) {
-      const int row = m0 + tid;
-      const bool ok = row >= 0 && row < p.Nq;
-      const float L = ok ? p.lse[b * p.ls[0] + hq * p.ls[1] + row * p.ls[2]] : 0.f;
-      lreg = (L == -INFINITY) ? 0.f : L * kLog2e;
-      dreg = ok ? p.delta[((int64_t)b * p.Hq + hq) * p.Nq + row] : 0.f;
+    st.load(tid, qrs, p.qts[2], ors, p.dos[2], m0);
+    if (tid < 64) {
+      const int row = m0 + (tid & 31);
+      const bool ok = row < p.Nq;
+      if (tid < 32) {
+        const float L = ok ? p.lse[b * p.ls[0] + hq * p.ls[1] + row * p.ls[2]] : 0.f;
+        lreg = (L == -INFINITY) ? 0.f : L * kLog2e;
+      } else {
+        dreg = ok ? p.delta[((int64_t)b * p.Hq + hq) * p.Nq + row] : 0.f;
+      }
     }
   };
   auto stage_store = [&](uint16_t* buf) {
-#pragma unroll
-    for (int i = 0; i < UPT; ++i) {
-      const int u = tid + i * NT;
-      if (u < QT::UNITS) qt[i].store(buf, buf + 2 * ROWS);
-      else if (u < 2 * QT::UNITS) ot[i].store(buf + ROWS, buf + 2 * ROWS + TRS);
-    }
-    float* f = reinterpret_cast<float*>(buf + 2 * ROWS + 2 * TRS);
-    if (tid < 32) {
-      f[tid] = lreg;
-      f[32 + tid] = dreg;
-    }
+    st.store(tid, buf);
+    float* f = reinterpret_cast<float*>(buf + 2 * TILE);
+    if (tid < 32) f[tid] = lreg;
+    else if (tid < 64) f[tid] = dreg;
   };
 
   f32x16 dk[DB], dv[DB];
@@ -365,6 +399,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   }
   const float c2 = p.scale * kLog2e;
   constexpr bool kAlibiOneSided = BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW);
+  const int qr_row = kperm(c);   // tile row of this lane's (permuted) query
 
   if (ntiles > 0) {
     stage_load(0);
@@ -378,10 +413,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
     const int m0 = tile_m0(t - gi * ntq);
     const uint16_t* buf = lds + (t & 1) * STAGE;
     const uint16_t* Qs = buf;
-    const uint16_t* dOs = buf + ROWS;
-    const uint16_t* Qt = buf + 2 * ROWS;
-    const uint16_t* dOt = buf + 2 * ROWS + TRS;
-    const float* Ls = reinterpret_cast<const float*>(buf + 2 * ROWS + 2 * TRS);
+    const uint16_t* Os = buf + TILE;
+    const float* Ls = reinterpret_cast<const float*>(buf + 2 * TILE);
     const float* Dl = Ls + 32;
 
     bool active = n0w < p.Nkv && m0 < p.Nq;
@@ -391,12 +424,14 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
     if (active) {
       // S and dP (queries x keys), query rows permuted.
       f32x16 s = f32x16{}, dp = f32x16{};
-      const uint16_t* qrow = Qs + kperm(c) * RP + 8 * h;
-      const uint16_t* orow = dOs + kperm(c) * RP + 8 * h;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        s = E::mfma32(ld16(qrow + 16 * ks), kf[ks], s);
-        dp = E::mfma32(ld16(orow + 16 * ks), vf[ks], dp);
+        const int off = lds_at<D>(qr_row, 16 * ks + 8 * h);
+        s = E::mfma32(ld16(Qs + off), kf[ks], s);
+        u32x4 vb;
+        if constexpr (VLDS) vb = ld16(vblk + 32 * w * D + off);
+        else vb = vf[ks];
+        dp = E::mfma32(ld16(Os + off), vb, dp);
       }
       float slope2 = 0.f;
       if constexpr (BIAS == BIAS_ALIBI) slope2 = p.slopes[hq] * kLog2e;
@@ -457,15 +492,19 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
           pd[j][i] = E::pack(dsv[2 * i], dsv[2 * i + 1]);
         }
       }
-      // dV^T += dO^T P,  dK~^T += Q~^T dS   (contraction over 32 queries)
+      // dV^T += dO^T P,  dK~^T += Q~^T dS   (contraction over 32 queries;
+      // the transposed operands come from transposing LDS reads)
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const uint16_t* otr = dOt + (32 * db + c) * TP + 8 * h;
-        const uint16_t* qtr = Qt + (32 * db + c) * TP + 8 * h;
+        const int t0 = tr_at<D>(lane, 0, db), t1 = tr_at<D>(lane, 1, db);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          dv[db] = E::mfma32(ld16(otr + 16 * j), pp[j], dv[db]);
-          dk[db] = E::mfma32(ld16(qtr + 16 * j), pd[j], dk[db]);
+          const u32x2 olo = lds_read_tr16(Os + 16 * j * D + t0);
+          const u32x2 ohi = lds_read_tr16(Os + 16 * j * D + t1);
+          dv[db] = E::mfma32(u32x4{olo[0], olo[1], ohi[0], ohi[1]}, pp[j], dv[db]);
+          const u32x2 qlo = lds_read_tr16(Qs + 16 * j * D + t0);
+          const u32x2 qhi = lds_read_tr16(Qs + 16 * j * D + t1);
+          dk[db] = E::mfma32(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]}, pd[j], dk[db]);
         }
       }
     }
@@ -487,17 +526,13 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   constexpr int NT = WAVES * 64;
   constexpr int BMq = 32 * WAVES;
   constexpr int KS = D / 16, DB = D / 32;
-  using KT = Tile32<E, D, ROPE, true>;
-  using VT = Tile32<E, D, false, false>;
-  constexpr int RP = KT::RP, TP = KT::TP;
-  constexpr int ROWS = 32 * RP, TRS = D * TP;
-  constexpr int STAGE = 2 * ROWS + TRS;
-  constexpr int UPT = (2 * KT::UNITS + NT - 1) / NT;
+  constexpr int TILE = 32 * D;
+  constexpr int STAGE = 2 * TILE;   // k~ tile, v tile
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
   // no queries: nothing to write (the launch still has one workgroup)
   if (p.n_qblocks <= 0) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
   const int BH = p.B * p.Hq;
   const int bh = blockIdx.x % BH;
   const int mbi = blockIdx.x / BH;
@@ -507,10 +542,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   const int m0 = mb * BMq, q0w = m0 + 32 * w, qrow = q0w + c;
 
   u32x4 qf[KS], of[KS];
-  load_operand_rows<E, D, ROPE>(qf, p.q + b * p.qs[0] + hq * p.qs[1], p.qs[2], qrow, p.Nq, p.cos, p.sin, p.rs[0],
-                                h);
-  load_operand_rows<E, D, false>(of, p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], qrow, p.Nq, nullptr,
-                                 nullptr, 0, h);
+  load_operand_rows<D>(qf, p.qt + b * p.qts[0] + hq * p.qts[1], p.qts[2], qrow, p.Nq, h);
+  load_operand_rows<D>(of, p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], qrow, p.Nq, h);
   float L2 = 0.f, dl = 0.f;
   if (qrow < p.Nq) {
     const float L = p.lse[b * p.ls[0] + hq * p.ls[1] + qrow * p.ls[2]];
@@ -550,34 +583,10 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
     }
   };
 
-  const uint16_t* kbase = p.k + b * p.ks[0] + hk * p.ks[1];
-  const uint16_t* vbase = p.v + b * p.vs[0] + hk * p.vs[1];
-  KT kt[UPT];
-  VT vt[UPT];
-  const auto krs = make_rsrc(kbase, span_bytes<D>(p.Nkv, p.ks[2]));
-  const auto vrs = make_rsrc(vbase, span_bytes<D>(p.Nkv, p.vs[2]));
-  const uint32_t rope_bytes = ROPE ? span_bytes<D>(p.rope_len, p.rs[0]) : 0u;
-  const auto crs = make_rsrc(p.cos, rope_bytes);
-  const auto srs = make_rsrc(p.sin, rope_bytes);
-  auto stage_load = [&](int t) {
-    const int n0 = tile_n0(t);
-#pragma unroll
-    for (int i = 0; i < UPT; ++i) {
-      const int u = tid + i * NT;
-      if (u < KT::UNITS)
-        kt[i].load(u, krs, p.ks[2], n0, crs, srs, p.rs[0]);
-      else if (u < 2 * KT::UNITS)
-        vt[i].load(u - KT::UNITS, vrs, p.vs[2], n0, crs, srs, 0);
-    }
-  };
-  auto stage_store = [&](uint16_t* buf) {
-#pragma unroll
-    for (int i = 0; i < UPT; ++i) {
-      const int u = tid + i * NT;
-      if (u < KT::UNITS) kt[i].store(buf, buf + 2 * ROWS);
-      else if (u < 2 * KT::UNITS) vt[i].store(buf + ROWS, nullptr);
-    }
-  };
+  const auto krs = make_rsrc(p.kt + b * p.kts[0] + hk * p.kts[1], span_bytes<D>(p.Nkv, p.kts[2]));
+  const auto vrs = make_rsrc(p.v + b * p.vs[0] + hk * p.vs[1], span_bytes<D>(p.Nkv, p.vs[2]));
+  TilePair<D, NT> st;
+  auto stage_load = [&](int t) { st.load(tid, krs, p.kts[2], vrs, p.vs[2], tile_n0(t)); };
 
   f32x16 dq[DB];
 #pragma unroll
@@ -586,20 +595,19 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   float slope2 = 0.f;
   if constexpr (BIAS == BIAS_ALIBI) slope2 = p.slopes[hq] * kLog2e;
   constexpr bool kAlibiOneSided = BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW);
+  const int kr_row = kperm(c);   // tile row of this lane's (permuted) key
 
   if (ntiles > 0) {
     stage_load(0);
-    stage_store(lds);
+    st.store(tid, lds);
   }
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const bool more = t + 1 < ntiles;
     if (more) stage_load(t + 1);
     const int n0 = tile_n0(t);
-    const uint16_t* buf = lds + (t & 1) * STAGE;
-    const uint16_t* Ks = buf;
-    const uint16_t* Vs = buf + ROWS;
-    const uint16_t* Kt = buf + 2 * ROWS;
+    const uint16_t* Ks = lds + (t & 1) * STAGE;
+    const uint16_t* Vs = Ks + TILE;
 
     bool active = q0w < p.Nq && n0 >= 0 && n0 < p.Nkv;
     if constexpr (MASK == MASK_CAUSAL) active = active && n0 <= q0w + 31;
@@ -607,12 +615,11 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
     if constexpr (MASK == MASK_CSW) active = active && n0 + 31 > q0w - p.window && n0 <= q0w + 31;
     if (active) {
       f32x16 s = f32x16{}, dp = f32x16{};
-      const uint16_t* krow = Ks + kperm(c) * RP + 8 * h;
-      const uint16_t* vrow = Vs + kperm(c) * RP + 8 * h;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        s = E::mfma32(ld16(krow + 16 * ks), qf[ks], s);
-        dp = E::mfma32(ld16(vrow + 16 * ks), of[ks], dp);
+        const int off = lds_at<D>(kr_row, 16 * ks + 8 * h);
+        s = E::mfma32(ld16(Ks + off), qf[ks], s);
+        dp = E::mfma32(ld16(Vs + off), of[ks], dp);
       }
       bool need_mask = q0w + 32 > p.Nq || n0 + 32 > p.Nkv;
       if constexpr (MASK == MASK_CAUSAL) need_mask = need_mask || n0 + 31 > q0w;
@@ -657,14 +664,19 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) pd[j][i] = E::pack(dsv[2 * i], dsv[2 * i + 1]);
       }
+      // dQ~^T += K~^T dS^T (contraction over 32 keys, K~^T by transposing reads)
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const uint16_t* ktr = Kt + (32 * db + c) * TP + 8 * h;
+        const int t0 = tr_at<D>(lane, 0, db), t1 = tr_at<D>(lane, 1, db);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) dq[db] = E::mfma32(ld16(ktr + 16 * j), pd[j], dq[db]);
+        for (int j = 0; j < 2; ++j) {
+          const u32x2 klo = lds_read_tr16(Ks + 16 * j * D + t0);
+          const u32x2 khi = lds_read_tr16(Ks + 16 * j * D + t1);
+          dq[db] = E::mfma32(u32x4{klo[0], klo[1], khi[0], khi[1]}, pd[j], dq[db]);
+        }
       }
     }
-    if (more) stage_store(lds + ((t + 1) & 1) * STAGE);
+    if (more) st.store(tid, lds + ((t + 1) & 1) * STAGE);
     __syncthreads();
   }
 

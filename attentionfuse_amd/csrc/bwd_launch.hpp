@@ -11,11 +11,17 @@
 namespace af {
 
 struct BwdGrids {
-  unsigned delta, dkv, dq;
+  unsigned prep, dkv, dq;
   int waves_kv, waves_q;
 };
 
-size_t bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q);
+// Workspace layout: delta (fp32, B*Hq*Nq), then with RoPE q~ (B*Hq*Nq*D) and
+// k~ (B*Hkv*Nkv*D) in the input dtype; each section 256-byte aligned.
+struct BwdWorkspace {
+  size_t delta, qr, kr, total;   // byte offsets and size
+};
+BwdWorkspace bwd_workspace_layout(const af_bwd_args& a);
+size_t bwd_workspace_bytes(const af_bwd_args& a);
 int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_t workspace_bytes,
             hipStream_t stream);
 

@@ -99,7 +99,7 @@ SIGNATURES = {
     "af_decode_workspace_bytes": (C.c_size_t, [C.c_int32] * 4),
     "af_decode": (C.c_int, [C.POINTER(DecodeArgsC), C.c_void_p, C.c_size_t,
                             C.c_void_p]),
-    "af_bwd_workspace_bytes": (C.c_size_t, [C.c_int32] * 3),
+    "af_bwd_workspace_bytes": (C.c_size_t, [C.POINTER(BwdArgsC)]),
     "af_bwd": (C.c_int, [C.POINTER(BwdArgsC), C.POINTER(BlockMaskC),
                          C.c_void_p, C.c_size_t, C.c_void_p]),
     "af_query": (C.c_int, [C.POINTER(SpecKeyC)]),
@@ -109,7 +109,7 @@ SIGNATURES = {
     "af_abi_version": (C.c_int, []),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 _lock = threading.Lock()

@@ -73,7 +73,7 @@ def _run_backward_key(key, Q, K, V, O, L, dO, sm_scale, window, cos, sin,
     a.rope_len = 0 if c is None else c.shape[0]
     a.scale = float(sm_scale)
     a.window = int(window or 0)
-    nbytes = int(N.lib().af_bwd_workspace_bytes(B, Hq, Nq))
+    nbytes = int(N.lib().af_bwd_workspace_bytes(a))
     ws = _bwd_workspace(Q.device, nbytes)
     bm = block_mask._c() if block_mask is not None else None
     N.check(N.lib().af_bwd(a, bm, ws.data_ptr(), ws.numel(),

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define AF_ABI_VERSION 1
+#define AF_ABI_VERSION 2
 
 typedef enum af_status {
   AF_OK = 0,
@@ -174,8 +174,9 @@ typedef struct af_bwd_args {
   int32_t window;
 } af_bwd_args;
 
-size_t af_bwd_workspace_bytes(int32_t batch, int32_t heads_q,
-                              int32_t seqlen_q);
+/* Workspace bytes af_bwd needs for these arguments: delta (fp32 per query
+ * row) and, with fused RoPE, the rotated q~ and k~ in the input dtype. */
+size_t af_bwd_workspace_bytes(const af_bwd_args* args);
 int af_bwd(const af_bwd_args* args, const af_blockmask* bm /* nullable */,
            void* workspace, size_t workspace_bytes, void* stream);
 
