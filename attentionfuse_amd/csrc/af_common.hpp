@@ -151,6 +151,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 __device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
 }
+// 16 bytes per lane from the buffer straight into LDS (buffer_load ... lds):
+// lane l's bytes land at lds_base + 16 l.  lds_base must be wave-uniform.
+// Kept out of templates: the host pass of a template that names this builtin
+// rejects later instantiations of the same template.
+__device__ __forceinline__ void buf_ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds_base,
+                                             uint32_t byte_off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base,
+                                           16, byte_off, 0, 0, 0);
+}
 
 // ---------------------------------------------------------------------------
 // Transposed LDS read (ds_read_b64_tr_b16).  Within each 16-lane group,

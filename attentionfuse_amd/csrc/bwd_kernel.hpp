@@ -254,39 +254,48 @@ __device__ __forceinline__ bool visible(int i, int j, int Nq, int Nkv, int W) {
 }
 
 // Staging of two 32-row tiles (rows [r0, r0 + 32) of tensors A and B, D
-// elements each) through registers into one swizzled LDS stage: tile A at
-// buf, tile B at buf + 32 D.
+// elements each) straight from global memory into one swizzled LDS stage --
+// tile A at element 0 of the stage, tile B at element 32 D -- with
+// buffer_load ... lds: one wave instruction fills 64 consecutive 16-byte LDS
+// chunks (lane l at chunk l), so each lane fetches the logical chunk that its
+// slot holds under the swizzle.  No data passes through registers.  Rows past
+// the end of a tensor fall outside its resource and load as zeros.
 template <int D, int NT>
-struct TilePair {
-  static constexpr int CHUNKS = 32 * D / 8;               // per tensor
-  static constexpr int CPT = (2 * CHUNKS + NT - 1) / NT;  // per thread
-  u32x4 x[CPT];
+struct TileDma {
+  static constexpr int CHUNKS = 32 * D / 8;          // per tensor, a multiple of 64
+  static constexpr int INSTR = 2 * CHUNKS / 64;      // wave instructions per stage
+  static constexpr int WAVES = NT / 64;
+  static constexpr int IPW = (INSTR + WAVES - 1) / WAVES;
+  uint32_t off[IPW];                                 // byte offsets within rows [r0, r0 + 32)
 
-  __device__ void load(int tid, __amdgpu_buffer_rsrc_t ar, int64_t astride, __amdgpu_buffer_rsrc_t br,
-                       int64_t bstride, int r0) {
+  __device__ void init(int w, int lane, int64_t astride, int64_t bstride) {
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int g = tid + i * NT;
-      if (2 * CHUNKS % NT != 0 && g >= 2 * CHUNKS) continue;
-      const int rem = g % CHUNKS;
-      const int row = rem / (D / 8), k = rem % (D / 8);
-      if (g < CHUNKS)
-        x[i] = buf_ld16(ar, (uint32_t)(((r0 + row) * astride + 8 * k) * 2));
-      else
-        x[i] = buf_ld16(br, (uint32_t)(((r0 + row) * bstride + 8 * k) * 2));
+    for (int i = 0; i < IPW; ++i) {
+      const int m = w + i * WAVES;
+      const int pos = 64 * m + lane;
+      const bool isb = pos >= CHUNKS;
+      const int rem = isb ? pos - CHUNKS : pos;
+      const int row = rem / (D / 8), kp = rem % (D / 8);
+      off[i] = (uint32_t)((row * (isb ? bstride : astride) + 8 * (kp ^ lds_swz<D>(row))) * 2);
     }
   }
-  __device__ void store(int tid, uint16_t* buf) const {
+  // stage = element offset of the stage inside `lds`
+  __device__ void load(uint16_t* lds, int stage, int w, const uint16_t* abase, int64_t astride, int an,
+                       const uint16_t* bbase, int64_t bstride, int bn, int r0) const {
+    const auto ar = make_rsrc(abase + (int64_t)r0 * astride, span_bytes<D>(an - r0, astride));
+    const auto br = make_rsrc(bbase + (int64_t)r0 * bstride, span_bytes<D>(bn - r0, bstride));
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int g = tid + i * NT;
-      if (2 * CHUNKS % NT != 0 && g >= 2 * CHUNKS) continue;
-      const int rem = g % CHUNKS;
-      const int row = rem / (D / 8), k = rem % (D / 8);
-      st16(buf + (g >= CHUNKS ? 32 * D : 0) + lds_at<D>(row, 8 * k), x[i]);
+    for (int i = 0; i < IPW; ++i) {
+      const int m = w + i * WAVES;   // wave-uniform
+      if (INSTR % WAVES != 0 && m >= INSTR) break;
+      buf_ld16_lds(64 * m >= CHUNKS ? br : ar, lds + stage + 512 * m, off[i]);
     }
   }
 };
+
+// Wait until this wave's loads into LDS have landed (the barrier after it
+// then publishes the whole stage).
+__device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---------------------------------------------------------------------------
 // dK / dV
@@ -304,7 +313,10 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
 
   // no keys: nothing to write (the launch still has one workgroup)
   if (p.n_kblocks <= 0) return;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
+  // the wave index is made provably uniform: it selects buffer resources and
+  // LDS bases of the loads into LDS, which must be scalar
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   // key block outermost: under a causal mask the first key blocks see the
   // most query tiles, so they are dispatched first.
   const int BHK = p.B * p.Hkv;
@@ -365,14 +377,15 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   };
   const int ntiles = ntq * p.G;
 
-  TilePair<D, NT> st;
+  TileDma<D, NT> dma;
+  dma.init(w, lane, p.qts[2], p.dos[2]);
   float lreg = 0.f, dreg = 0.f;
-  auto stage_load = [&](int t) {
+  // issue the tile loads of stage t into LDS slot `slot`, and fetch its L / delta
+  auto stage_load = [&](int t, int slot) {
     const int gi = t / ntq, hq = hk * p.G + gi;
     const int m0 = tile_m0(t - gi * ntq);
-    const auto qrs = make_rsrc(p.qt + b * p.qts[0] + hq * p.qts[1], span_bytes<D>(p.Nq, p.qts[2]));
-    const auto ors = make_rsrc(p.dout + b * p.dos[0] + hq * p.dos[1], span_bytes<D>(p.Nq, p.dos[2]));
-    st.load(tid, qrs, p.qts[2], ors, p.dos[2], m0);
+    dma.load(lds, slot * STAGE, w, p.qt + b * p.qts[0] + hq * p.qts[1], p.qts[2], p.Nq,
+             p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], p.Nq, m0);
     if (tid < 64) {
       const int row = m0 + (tid & 31);
       const bool ok = row < p.Nq;
@@ -384,9 +397,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
       }
     }
   };
-  auto stage_store = [&](uint16_t* buf) {
-    st.store(tid, buf);
-    float* f = reinterpret_cast<float*>(buf + 2 * TILE);
+  auto stage_store = [&](int slot) {
+    float* f = reinterpret_cast<float*>(lds + slot * STAGE + 2 * TILE);
     if (tid < 32) f[tid] = lreg;
     else if (tid < 64) f[tid] = dreg;
   };
@@ -402,13 +414,14 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   const int qr_row = kperm(c);   // tile row of this lane's (permuted) query
 
   if (ntiles > 0) {
-    stage_load(0);
-    stage_store(lds);
+    stage_load(0, 0);
+    stage_store(0);
   }
+  wait_lds_dma();
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const bool more = t + 1 < ntiles;
-    if (more) stage_load(t + 1);
+    if (more) stage_load(t + 1, (t + 1) & 1);
     const int gi = t / ntq, hq = hk * p.G + gi;
     const int m0 = tile_m0(t - gi * ntq);
     const uint16_t* buf = lds + (t & 1) * STAGE;
@@ -508,7 +521,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
         }
       }
     }
-    if (more) stage_store(lds + ((t + 1) & 1) * STAGE);
+    if (more) stage_store((t + 1) & 1);
+    wait_lds_dma();
     __syncthreads();
   }
 
@@ -532,7 +546,10 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
 
   // no queries: nothing to write (the launch still has one workgroup)
   if (p.n_qblocks <= 0) return;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
+  // the wave index is made provably uniform: it selects buffer resources and
+  // LDS bases of the loads into LDS, which must be scalar
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int BH = p.B * p.Hq;
   const int bh = blockIdx.x % BH;
   const int mbi = blockIdx.x / BH;
@@ -583,10 +600,13 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
     }
   };
 
-  const auto krs = make_rsrc(p.kt + b * p.kts[0] + hk * p.kts[1], span_bytes<D>(p.Nkv, p.kts[2]));
-  const auto vrs = make_rsrc(p.v + b * p.vs[0] + hk * p.vs[1], span_bytes<D>(p.Nkv, p.vs[2]));
-  TilePair<D, NT> st;
-  auto stage_load = [&](int t) { st.load(tid, krs, p.kts[2], vrs, p.vs[2], tile_n0(t)); };
+  TileDma<D, NT> dma;
+  dma.init(w, lane, p.kts[2], p.vs[2]);
+  const uint16_t* kbase = p.kt + b * p.kts[0] + hk * p.kts[1];
+  const uint16_t* vbase = p.v + b * p.vs[0] + hk * p.vs[1];
+  auto stage_load = [&](int t, int slot) {
+    dma.load(lds, slot * STAGE, w, kbase, p.kts[2], p.Nkv, vbase, p.vs[2], p.Nkv, tile_n0(t));
+  };
 
   f32x16 dq[DB];
 #pragma unroll
@@ -597,14 +617,12 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   constexpr bool kAlibiOneSided = BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW);
   const int kr_row = kperm(c);   // tile row of this lane's (permuted) key
 
-  if (ntiles > 0) {
-    stage_load(0);
-    st.store(tid, lds);
-  }
+  if (ntiles > 0) stage_load(0, 0);
+  wait_lds_dma();
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const bool more = t + 1 < ntiles;
-    if (more) stage_load(t + 1);
+    if (more) stage_load(t + 1, (t + 1) & 1);
     const int n0 = tile_n0(t);
     const uint16_t* Ks = lds + (t & 1) * STAGE;
     const uint16_t* Vs = Ks + TILE;
@@ -676,7 +694,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
         }
       }
     }
-    if (more) st.store(tid, lds + ((t + 1) & 1) * STAGE);
+    wait_lds_dma();
     __syncthreads();
   }
 
