@@ -256,4 +256,87 @@ __device__ __forceinline__ void st16(void* p, u32x4 v) {
   *reinterpret_cast<u32x4*>(p) = v;
 }
 
+// Byte range of `rows` rows of D elements at `rstride` elements apart.
+template <int D>
+__device__ __forceinline__ uint32_t span_bytes(int rows, int64_t rstride) {
+  return rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * rstride + D) * 2) : 0u;
+}
+
+// ---------------------------------------------------------------------------
+// LDS tile swizzle.  A tile row holds D elements = D/8 chunks of 16 bytes;
+// logical chunk k of row r is stored at chunk k ^ lds_swz<D>(r).  The
+// function depends on r mod 16 only, so tiles can be addressed at 16-row
+// offsets without re-swizzling.  Chosen so that (a) 16 lanes reading the
+// same chunk of 16 different rows (the MFMA row operands) and (b) the
+// 32-lane passes of ds_read_b64_tr_b16 (4 rows x 4 consecutive chunks) each
+// touch 64 distinct banks.
+// ---------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ int lds_swz(int r) {
+  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else if constexpr (D == 64) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else return (r >> 2) & 3;
+}
+// element offset of element `col` of row `r`
+template <int D>
+__device__ __forceinline__ int lds_at(int r, int col) {
+  return r * D + 8 * ((col >> 3) ^ lds_swz<D>(r)) + (col & 7);
+}
+// Per-lane offset of the two ds_read_b64_tr_b16 (t = 0, 1) that together
+// give this lane the 32x32x16 A operand X^T[32 db + l%32][rows 8h .. 8h+7]
+// of the first 16 rows of a row-major, swizzled (rows x D) tile -- the
+// read pattern tr_source_offset describes for padded tiles.  Add 16*j*D
+// for rows 16j .. 16j+15.
+template <int D>
+__device__ __forceinline__ int tr_at(int lane, int t, int db) {
+  const int row = 8 * (lane >> 5) + 4 * t + ((lane & 15) >> 2);
+  const int col = 32 * db + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  return lds_at<D>(row, col);
+}
+
+// Staging of two row tiles (rows [r0, r0 + ROWS) of tensors A and B, D
+// elements each) straight from global memory into one swizzled LDS stage --
+// tile A at element 0 of the stage, tile B at element ROWS * D -- with
+// buffer_load ... lds: one wave instruction fills 64 consecutive 16-byte LDS
+// chunks (lane l at chunk l), so each lane fetches the logical chunk that its
+// slot holds under the swizzle.  No data passes through registers.  Rows past
+// the end of a tensor fall outside its resource and load as zeros.
+template <int D, int NT, int ROWS = 32>
+struct TileDma {
+  static_assert(ROWS % 16 == 0 && ROWS * D % 512 == 0, "whole wave instructions per tile");
+  static constexpr int CHUNKS = ROWS * D / 8;        // per tensor, a multiple of 64
+  static constexpr int INSTR = 2 * CHUNKS / 64;      // wave instructions per stage
+  static constexpr int WAVES = NT / 64;
+  static constexpr int IPW = (INSTR + WAVES - 1) / WAVES;
+  uint32_t off[IPW];                                 // byte offsets within rows [r0, r0 + ROWS)
+
+  __device__ void init(int w, int lane, int64_t astride, int64_t bstride) {
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int m = w + i * WAVES;
+      const int pos = 64 * m + lane;
+      const bool isb = pos >= CHUNKS;
+      const int rem = isb ? pos - CHUNKS : pos;
+      const int row = rem / (D / 8), kp = rem % (D / 8);
+      off[i] = (uint32_t)((row * (isb ? bstride : astride) + 8 * (kp ^ lds_swz<D>(row))) * 2);
+    }
+  }
+  // stage = element offset of the stage inside `lds`
+  __device__ void load(uint16_t* lds, int stage, int w, const uint16_t* abase, int64_t astride, int an,
+                       const uint16_t* bbase, int64_t bstride, int bn, int r0) const {
+    const auto ar = make_rsrc(abase + (int64_t)r0 * astride, span_bytes<D>(an - r0, astride));
+    const auto br = make_rsrc(bbase + (int64_t)r0 * bstride, span_bytes<D>(bn - r0, bstride));
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int m = w + i * WAVES;   // wave-uniform
+      if (INSTR % WAVES != 0 && m >= INSTR) break;
+      buf_ld16_lds(64 * m >= CHUNKS ? br : ar, lds + stage + 512 * m, off[i]);
+    }
+  }
+};
+
+// Wait until this wave's loads into LDS have landed (the barrier after it
+// then publishes the whole stage).
+__device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 }  // namespace af

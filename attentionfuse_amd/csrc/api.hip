@@ -131,19 +131,60 @@ bool slice_fits_u32(int64_t rows, int64_t row_stride, int d) {
   return rows <= 0 || ((rows - 1) * row_stride + d) * 2 < (int64_t(1) << 32);
 }
 
+size_t fwd_workspace_bytes(const af_fwd_args& a) {
+  if (!a.key.rope || a.batch <= 0 || a.heads_kv <= 0 || a.seqlen_kv <= 0 || a.key.head_dim <= 0) return 0;
+  const size_t bytes = (size_t)a.batch * a.heads_kv * a.seqlen_kv * a.key.head_dim * 2;
+  return (bytes + 255) & ~size_t(255);
+}
+
+// With RoPE, rotate K once into the workspace and point the forward at k~.
+int rotate_keys(FwdParams& p, const af_fwd_args& a, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  const size_t need = fwd_workspace_bytes(a);
+  if (need == 0) return AF_OK;
+  if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+    return fail(AF_ERR_WORKSPACE, "forward with RoPE needs a %zu-byte workspace (16-byte aligned), got %zu", need,
+                workspace_bytes);
+  const int D = a.key.head_dim;
+  RopeRowsParams r;
+  r.x = static_cast<const uint16_t*>(a.k);
+  r.out = static_cast<uint16_t*>(workspace);
+  r.cos = static_cast<const uint16_t*>(a.cos);
+  r.sin = static_cast<const uint16_t*>(a.sin);
+  for (int i = 0; i < 3; ++i) r.xs[i] = a.k_stride[i];
+  r.rs = a.rope_stride[0];
+  r.rows = (int64_t)a.batch * a.heads_kv * a.seqlen_kv;
+  r.H = a.heads_kv;
+  r.N = a.seqlen_kv;
+  const bool f16 = a.key.dtype == AF_F16;
+  switch (D) {
+    case 32: f16 ? launch_rope_f16_d32(r, s) : launch_rope_bf16_d32(r, s); break;
+    case 64: f16 ? launch_rope_f16_d64(r, s) : launch_rope_bf16_d64(r, s); break;
+    case 128: f16 ? launch_rope_f16_d128(r, s) : launch_rope_bf16_d128(r, s); break;
+  }
+  p.k = r.out;
+  p.ks[3] = 1;
+  p.ks[2] = D;
+  p.ks[1] = (int64_t)a.seqlen_kv * D;
+  p.ks[0] = (int64_t)a.heads_kv * a.seqlen_kv * D;
+  return AF_OK;
+}
+
 // Waves (32 query rows each) per forward workgroup for dense / causal /
 // windowed masks.  Measured on MI355X at D = 64: 8-wave workgroups (one per
 // CU) lose to two 4-wave workgroups per CU, whose barriers do not line up.
 int fwd_waves(const af_spec_key&) { return 4; }
 
-int dispatch_fwd(const FwdParams& p, const af_spec_key& k, int waves, hipStream_t s) {
-  if (!slice_fits_u32(p.Nkv, p.ks[2], k.head_dim) || !slice_fits_u32(p.Nkv, p.vs[2], k.head_dim) ||
-      (k.rope && !slice_fits_u32(p.rope_len, p.rs[0], k.head_dim)))
-    return fail(AF_ERR_UNSUPPORTED, "a (batch, head) slice of K, V or the RoPE tables spans 4 GiB or more");
+int dispatch_fwd(FwdParams p, const af_fwd_args& a, int waves, void* workspace, size_t workspace_bytes,
+                 hipStream_t s) {
+  const af_spec_key& k = a.key;
+  if (!slice_fits_u32(p.Nkv, p.ks[2], k.head_dim) || !slice_fits_u32(p.Nkv, p.vs[2], k.head_dim))
+    return fail(AF_ERR_UNSUPPORTED, "a (batch, head) slice of K or V spans 4 GiB or more");
   if (!(p.scale > 0.f) || p.scale == INFINITY)
     return fail(AF_ERR_BAD_ARG, "scale must be positive and finite (got %g)", (double)p.scale);
+  int rc = rotate_keys(p, a, workspace, workspace_bytes, s);
+  if (rc) return rc;
   const dim3 grid((unsigned)p.n_mblocks * (unsigned)(p.B * p.Hq));
-  int rc = -1;
+  rc = -1;
   const bool f16 = k.dtype == AF_F16;
   switch (k.head_dim) {
     case 32:
@@ -190,17 +231,22 @@ int af_fwd_tile(const af_spec_key* key, int32_t* block_m, int32_t* block_n) {
   return AF_OK;
 }
 
-int af_fwd(const af_fwd_args* a, void* stream) {
+size_t af_fwd_workspace_bytes(const af_fwd_args* args) {
+  return args == nullptr ? 0 : fwd_workspace_bytes(*args);
+}
+
+int af_fwd(const af_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_fwd_common(a);
   if (rc) return rc;
   if ((rc = check_key(a->key, false))) return rc;
   if (a->seqlen_q == 0) return AF_OK;
   const int waves = fwd_waves(a->key);
   const FwdParams p = make_fwd_params(a, 32 * waves);
-  return dispatch_fwd(p, a->key, waves, static_cast<hipStream_t>(stream));
+  return dispatch_fwd(p, *a, waves, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
-int af_fwd_blocksparse(const af_fwd_args* a, const af_blockmask* bm, void* stream) {
+int af_fwd_blocksparse(const af_fwd_args* a, const af_blockmask* bm, void* workspace, size_t workspace_bytes,
+                       void* stream) {
   int rc = check_fwd_common(a);
   if (rc) return rc;
   if ((rc = check_key(a->key, true))) return rc;
@@ -226,7 +272,7 @@ int af_fwd_blocksparse(const af_fwd_args* a, const af_blockmask* bm, void* strea
   p.bs_full_rs = bm->full_kv_stride;
   p.bs_part_rs = bm->kv_stride;
   p.bs_block_n = bm->block_n;
-  return dispatch_fwd(p, a->key, bm->block_m / 32, static_cast<hipStream_t>(stream));
+  return dispatch_fwd(p, *a, bm->block_m / 32, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 int32_t af_decode_num_splits(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seqlen_kv,

@@ -20,6 +20,8 @@ using Elem = BF16;
 
 #define AF_FN_(dt, d) launch_fwd_##dt##_d##d
 #define AF_FN(dt, d) AF_FN_(dt, d)
+#define AF_RFN_(dt, d) launch_rope_##dt##_d##d
+#define AF_RFN(dt, d) AF_RFN_(dt, d)
 
 namespace {
 
@@ -82,6 +84,14 @@ int AF_FN(AF_DT_NAME, AF_D)(const FwdParams& p, int mask, int bias, int norm,
     case MASK_CSW: return pick_bias<MASK_CSW>(p, bias, norm, rope, waves, grid, s);
     default: return -1;
   }
+}
+
+int AF_RFN(AF_DT_NAME, AF_D)(const RopeRowsParams& p, hipStream_t s) {
+  constexpr int rows_per_block = 256 / (AF_D / 16);
+  const int64_t blocks = (p.rows + rows_per_block - 1) / rows_per_block;
+  if (blocks <= 0) return 0;
+  hipLaunchKernelGGL((rope_rows_kernel<Elem, AF_D>), dim3((unsigned)blocks), dim3(256), 0, s, p);
+  return 0;
 }
 
 }  // namespace af

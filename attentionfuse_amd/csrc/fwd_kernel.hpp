@@ -61,14 +61,6 @@ struct FwdParams {
   int32_t window;
 };
 
-// Row pitch (elements) of the row-major V stage: D/2 + 16 dwords (16 when
-// D = 32), i.e. 16 mod 32 dwords, so the eight rows one transposed read
-// touches spread over all 64 banks exactly twice.
-template <int D>
-constexpr int v_pitch() {
-  return D == 32 ? 32 : D + 32;
-}
-
 // Head dims up to 64 fit in 168 VGPRs (a few setup values spill outside the
 // loop): three waves per SIMD, three 4-wave workgroups per CU.
 template <class E, int D, int MASK, int BIAS, int NORM, bool ROPE, int WAVES>
@@ -77,23 +69,17 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   constexpr int NT = WAVES * 64;
   constexpr int BM = 32 * WAVES;
   constexpr int BN = 64;
-  constexpr int KP = D + 8;          // K stage row pitch (elements)
-  constexpr int VP = v_pitch<D>();   // V stage row pitch (elements)
   constexpr int KS = D / 16;         // 16-deep k-steps of Q K^T
   constexpr int DB = D / 32;         // 32-row blocks of O^T
-  constexpr int STAGE = BN * KP + BN * VP;  // elements per LDS stage
-  // K staging: rotate-half pairs (chunk j, chunk j + D/16) of one key row.
-  constexpr int KPAIRS = BN * D / 16;
-  constexpr int KPT = (KPAIRS + NT - 1) / NT;
-  // V staging: 16-byte chunks of the row-major tile.
-  constexpr int VCHUNKS = BN * D / 8;
-  constexpr int VPT = (VCHUNKS + NT - 1) / NT;
+  constexpr int TILE = BN * D;       // one swizzled (BN x D) tile, no padding
+  constexpr int STAGE = 2 * TILE;    // K tile, then V tile
 
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  // provably wave-uniform: it selects the LDS bases of the loads into LDS
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5;
   const int c = lane & 31;
 
@@ -176,68 +162,26 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     }
   };
 
-  // ---- staging through buffer resources ------------------------------------
-  // num_records covers rows [0, N_kv) of this (batch, kv head): any row
-  // outside loads as zeros (and its scores are masked anyway).
-  const uint32_t kbytes = p.Nkv > 0 ? (uint32_t)(((int64_t)(p.Nkv - 1) * kstr + D) * 2) : 0u;
-  const uint32_t vbytes = p.Nkv > 0 ? (uint32_t)(((int64_t)(p.Nkv - 1) * vstr + D) * 2) : 0u;
-  const auto krs = make_rsrc(kbase, kbytes);
-  const auto vrs = make_rsrc(vbase, vbytes);
-  const uint32_t rbytes = ROPE ? (uint32_t)(((int64_t)(p.rope_len - 1) * rstr + D) * 2) : 0u;
-  const auto crs = make_rsrc(p.cos, rbytes);
-  const auto srs = make_rsrc(p.sin, rbytes);
-
-  u32x4 kr[KPT][2];
-  u32x4 kc[ROPE ? KPT : 1][2], ksn[ROPE ? KPT : 1][2];
-  u32x4 vr[VPT];
-
-  auto stage_load = [&](int n0) {
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int pi = min(tid + i * NT, KPAIRS - 1);
-      const int row = pi / (D / 16), j = pi % (D / 16);
-      const int n = n0 + row;
-      const uint32_t ko = (uint32_t)((n * kstr + 8 * j) * 2);
-      kr[i][0] = buf_ld16(krs, ko);
-      kr[i][1] = buf_ld16(krs, ko + D);
-      if constexpr (ROPE) {
-        const uint32_t co = (uint32_t)((n * rstr + 8 * j) * 2);
-        kc[i][0] = buf_ld16(crs, co);
-        kc[i][1] = buf_ld16(crs, co + D);
-        ksn[i][0] = buf_ld16(srs, co);
-        ksn[i][1] = buf_ld16(srs, co + D);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int u = min(tid + i * NT, VCHUNKS - 1);
-      const int row = u / (D / 8), ch = u % (D / 8);
-      vr[i] = buf_ld16(vrs, (uint32_t)(((n0 + row) * vstr + 8 * ch) * 2));
-    }
+  // ---- K / V staging: buffer loads straight into the swizzled LDS stage ----
+  // Rows past N_kv fall outside the buffer resources and load as zeros (their
+  // scores are masked anyway).  With RoPE the K given here is already
+  // rotated (k~, written once per key by rope_rows_kernel).
+  TileDma<D, NT, BN> dma;
+  dma.init(w, lane, kstr, vstr);
+  auto stage_load = [&](int t) {
+    dma.load(lds, (t & 1) * STAGE, w, kbase, kstr, p.Nkv, vbase, vstr, p.Nkv, tile_n0(t));
   };
-  auto stage_store = [&](uint16_t* buf) {
-    uint16_t* Ks = buf;
-    uint16_t* Vs = buf + BN * KP;
+  // per-lane LDS offsets: the K rows of the S^T MFMA (key block 0; block 1 is
+  // 32 rows on, same swizzle) and the transposed V reads of the P V MFMA
+  int koff[KS];
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int pi = tid + i * NT;
-      if (KPAIRS % NT == 0 || pi < KPAIRS) {
-        const int row = pi / (D / 16), j = pi % (D / 16);
-        u32x4 lo = kr[i][0], hi = kr[i][1];
-        if constexpr (ROPE) rope_pair<E>(lo, hi, kc[i][0], ksn[i][0], kc[i][1], ksn[i][1]);
-        st16(Ks + row * KP + 8 * j, lo);
-        st16(Ks + row * KP + 8 * j + D / 2, hi);
-      }
-    }
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = lds_at<D>(kperm(c), 16 * ks + 8 * h);
+  int voff[DB][2];
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int u = tid + i * NT;
-      if (VCHUNKS % NT == 0 || u < VCHUNKS) {
-        const int row = u / (D / 8), ch = u % (D / 8);
-        st16(Vs + row * VP + 8 * ch, vr[i]);
-      }
-    }
-  };
+  for (int db = 0; db < DB; ++db) {
+    voff[db][0] = tr_at<D>(lane, 0, db);
+    voff[db][1] = tr_at<D>(lane, 1, db);
+  }
 
   // ---- online-softmax state ------------------------------------------------
   // Softmax runs in log2 units with a *lazy* running max: a row's m only
@@ -268,22 +212,16 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   const uint16_t* brow = nullptr;
   if constexpr (BIAS == BIAS_ADD) brow = p.bias + b * p.bs[0] + hq * p.bs[1] + (int64_t)qrow * p.bs[2];
 
-  // per-lane offsets of the transposed V reads (t = 0, 1)
-  const int vtr0 = tr_source_offset(lane, 0, VP);
-  const int vtr1 = tr_source_offset(lane, 1, VP);
-
-  if (ntiles > 0) {
-    stage_load(tile_n0(0));
-    stage_store(lds);
-  }
+  if (ntiles > 0) stage_load(0);
+  wait_lds_dma();
   __syncthreads();
 
   for (int t = 0; t < ntiles; ++t) {
     const int n0 = tile_n0(t);
     const bool more = t + 1 < ntiles;
-    if (more) stage_load(tile_n0(t + 1));
+    if (more) stage_load(t + 1);
     const uint16_t* Ks = lds + (t & 1) * STAGE;
-    const uint16_t* Vs = Ks + BN * KP;
+    const uint16_t* Vs = Ks + TILE;
 
     bool active = q0w < p.Nq && n0 >= 0 && n0 < p.Nkv;
     if constexpr (MASK == MASK_CAUSAL) active = active && n0 <= q0w + 31;
@@ -305,10 +243,9 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
       for (int kb = 0; kb < BN / 32; ++kb) {
         s[kb] = f32x16{};
-        const uint16_t* krow = Ks + (32 * kb + kperm(c)) * KP + 8 * h;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
-          s[kb] = E::mfma32(ld16(krow + 16 * ks), qf[ks], s[kb]);
+          s[kb] = E::mfma32(ld16(Ks + 32 * kb * D + koff[ks]), qf[ks], s[kb]);
       }
 
       bool need_mask = !active || n0 + BN > p.Nkv;
@@ -447,16 +384,18 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
       for (int db = 0; db < DB; ++db) {
 #pragma unroll
         for (int kk = 0; kk < BN / 16; ++kk) {
-          const uint16_t* vt = Vs + 16 * kk * VP + 32 * db;
-          const u32x2 lo = lds_read_tr16(vt + vtr0);
-          const u32x2 hi = lds_read_tr16(vt + vtr1);
+          const uint16_t* vt = Vs + 16 * kk * D;
+          const u32x2 lo = lds_read_tr16(vt + voff[db][0]);
+          const u32x2 hi = lds_read_tr16(vt + voff[db][1]);
           const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
           o[db] = E::mfma32(va, pf[kk], o[db]);
         }
       }
     }
 
-    if (more) stage_store(lds + ((t + 1) & 1) * STAGE);
+    // this wave's loads of stage t+1 have landed; after the barrier every
+    // wave's have, and no wave reads stage t any more
+    wait_lds_dma();
     __syncthreads();
   }
 

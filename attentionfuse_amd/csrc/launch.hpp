@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "fwd_kernel.hpp"
+#include "rope_kernel.hpp"
 
 namespace af {
 
@@ -25,5 +26,15 @@ AF_DECLARE_FWD(launch_fwd_bf16_d32)
 AF_DECLARE_FWD(launch_fwd_bf16_d64)
 AF_DECLARE_FWD(launch_fwd_bf16_d128)
 #undef AF_DECLARE_FWD
+
+// rope_rows_kernel launchers, defined next to the forward launchers.
+#define AF_DECLARE_ROPE(NAME) int NAME(const RopeRowsParams& p, hipStream_t stream);
+AF_DECLARE_ROPE(launch_rope_f16_d32)
+AF_DECLARE_ROPE(launch_rope_f16_d64)
+AF_DECLARE_ROPE(launch_rope_f16_d128)
+AF_DECLARE_ROPE(launch_rope_bf16_d32)
+AF_DECLARE_ROPE(launch_rope_bf16_d64)
+AF_DECLARE_ROPE(launch_rope_bf16_d128)
+#undef AF_DECLARE_ROPE
 
 }  // namespace af

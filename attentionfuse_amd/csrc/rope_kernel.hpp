@@ -1,0 +1,55 @@
+// Rotate-half RoPE of whole rows, written once to a contiguous buffer.
+//
+// x~[d]       = x[d] cos[n][d]       - x[d + D/2] sin[n][d]
+// x~[d + D/2] = x[d + D/2] cos[n][d + D/2] + x[d] sin[n][d + D/2]
+// rounded to the input dtype (reference: attnfuse/compiler/codegen.py:126-135
+// rotates the q and k tiles in registers and rounds them before Q K^T).
+//
+// The forward kernel rotates its query rows in registers (each is read once
+// per workgroup), but every key row is read by all query blocks of its head:
+// rotating it there repeats the rotation, and the cos/sin reads, once per
+// query block.  rope_rows_kernel rotates each key row exactly once instead;
+// the forward then streams k~ straight into LDS.
+#pragma once
+
+#include "af_common.hpp"
+
+namespace af {
+
+struct RopeRowsParams {
+  const uint16_t* x;      // (B, H, N, D), unit d-stride
+  uint16_t* out;          // (B, H, N, D) contiguous
+  const uint16_t* cos;    // (>= N, D) tables, row stride rs
+  const uint16_t* sin;
+  int64_t xs[3];          // batch, head and row strides of x (elements)
+  int64_t rs;
+  int64_t rows;           // B * H * N
+  int32_t H, N;
+};
+
+// Thread j of a row rotates the rotate-half pair (chunk j, chunk j + D/16).
+template <class E, int D>
+__device__ __forceinline__ void rope_row_chunk(const uint16_t* x, const uint16_t* cr, const uint16_t* sr,
+                                               uint16_t* out, int j) {
+  const int dl = 8 * j, dh = dl + D / 2;
+  u32x4 lo = ld16(x + dl), hi = ld16(x + dh);
+  rope_pair<E>(lo, hi, ld16(cr + dl), ld16(sr + dl), ld16(cr + dh), ld16(sr + dh));
+  st16(out + dl, lo);
+  st16(out + dh, hi);
+}
+
+template <class E, int D>
+__global__ void __launch_bounds__(256) rope_rows_kernel(const RopeRowsParams p) {
+  constexpr int TPR = D / 16;          // threads per row
+  constexpr int RPB = 256 / TPR;       // rows per workgroup
+  const int tid = threadIdx.x;
+  const int64_t r = (int64_t)blockIdx.x * RPB + tid / TPR;
+  if (r >= p.rows) return;
+  const int n = (int)(r % p.N);
+  const int64_t bh = r / p.N;
+  const int hh = (int)(bh % p.H), b = (int)(bh / p.H);
+  rope_row_chunk<E, D>(p.x + b * p.xs[0] + hh * p.xs[1] + n * p.xs[2], p.cos + n * p.rs, p.sin + n * p.rs,
+                       p.out + r * D, tid % TPR);
+}
+
+}  // namespace af

@@ -92,9 +92,12 @@ class BwdArgsC(C.Structure):
 
 # Every symbol the header declares, with its ctypes signature.
 SIGNATURES = {
-    "af_fwd": (C.c_int, [C.POINTER(FwdArgsC), C.c_void_p]),
+    "af_fwd_workspace_bytes": (C.c_size_t, [C.POINTER(FwdArgsC)]),
+    "af_fwd": (C.c_int, [C.POINTER(FwdArgsC), C.c_void_p, C.c_size_t,
+                         C.c_void_p]),
     "af_fwd_blocksparse": (C.c_int, [C.POINTER(FwdArgsC),
-                                     C.POINTER(BlockMaskC), C.c_void_p]),
+                                     C.POINTER(BlockMaskC), C.c_void_p,
+                                     C.c_size_t, C.c_void_p]),
     "af_decode_num_splits": (C.c_int32, [C.c_int32] * 5),
     "af_decode_workspace_bytes": (C.c_size_t, [C.c_int32] * 4),
     "af_decode": (C.c_int, [C.POINTER(DecodeArgsC), C.c_void_p, C.c_size_t,
@@ -109,7 +112,7 @@ SIGNATURES = {
     "af_abi_version": (C.c_int, []),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 _lock = threading.Lock()

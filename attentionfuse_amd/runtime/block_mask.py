@@ -146,8 +146,9 @@ def run_block_sparse(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
     """Block-sparse forward (reference signature,
     attnfuse/runtime/block_mask.py:205-210).  ``bias_kind`` 1 = ALiBi.
     ``cos``/``sin`` apply fused RoPE."""
-    from .dispatch import (_rows_ok, _slopes_f32, check_qkv, fill_fwd_args,
-                           kernel_layout, rope_tables)
+    from .dispatch import (_nbytes, _rows_ok, _slopes_f32, check_qkv,
+                           fill_fwd_args, fwd_workspace, kernel_layout,
+                           rope_tables)
     check_qkv(Q, K, V)
     _check_mask(Q, K, block_mask)
     B, H, Nq, D = Q.shape
@@ -165,7 +166,9 @@ def run_block_sparse(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
     fill_fwd_args(a, key, Qk, Kk, Vk, o, save_lse, c, s, slopes, None,
                   coverage, sm_scale, 0)
     bm = block_mask._c()
-    N.check(N.lib().af_fwd_blocksparse(a, bm, N.stream_handle(Q.device)))
+    ws = fwd_workspace(a, Q.device)
+    N.check(N.lib().af_fwd_blocksparse(a, bm, N.ptr(ws), _nbytes(ws),
+                                       N.stream_handle(Q.device)))
     if o is not out:
         out.copy_(o)
     return out

@@ -149,6 +149,18 @@ def fill_fwd_args(a: "N.FwdArgsC", key_tuple, Q, K, V, out, lse, c, s, slopes,
     a.window = int(window or 0)
 
 
+def fwd_workspace(args: "N.FwdArgsC", device) -> Optional[torch.Tensor]:
+    """Workspace the forward needs for these arguments (the rotated keys when
+    RoPE is fused), or None.  Allocated on the caller's stream through torch's
+    caching allocator, so releasing it after the launch is stream-ordered."""
+    n = int(N.lib().af_fwd_workspace_bytes(args))
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
+
+
+def _nbytes(ws: Optional[torch.Tensor]) -> int:
+    return 0 if ws is None else ws.numel()
+
+
 def run_attention(
     graph: Graph,
     Q: torch.Tensor,
@@ -217,7 +229,9 @@ def run_attention(
     args = N.FwdArgsC()
     fill_fwd_args(args, bundle.key.abi_tuple(), Qk, Kk, Vk, o, save_lse, c, s,
                   slopes, b, coverage, bundle.sm_scale, bundle.window)
-    N.check(N.lib().af_fwd(args, N.stream_handle(Q.device)))
+    ws = fwd_workspace(args, Q.device)
+    N.check(N.lib().af_fwd(args, N.ptr(ws), _nbytes(ws),
+                           N.stream_handle(Q.device)))
     if o is not out:
         out.copy_(o)
     return out

@@ -1,5 +1,6 @@
 """Prepared launches: validate and marshal a call once, then enqueue it any
-number of times with only a ctypes call of host work.
+number of times with only a ctypes call of host work (and the call's
+workspace allocated once).
 
 For fixed-shape loops (serving decode steps, benchmarks) the per-call
 Python dispatch of ``run_attention`` -- graph lookup, validation, layout
@@ -37,8 +38,9 @@ def prepare_attention(graph: Graph, Q, K, V, *, bias=None, cos=None, sin=None,
                       alibi_slopes=None) -> tuple:
     """-> (launch, out): ``launch()`` recomputes ``out`` from the current
     contents of Q/K/V (same shapes and storage)."""
-    from .dispatch import (_rows_ok, _slopes_f32, check_qkv, fill_fwd_args,
-                           kernel_layout, rope_tables)
+    from .dispatch import (_nbytes, _rows_ok, _slopes_f32, check_qkv,
+                           fill_fwd_args, fwd_workspace, kernel_layout,
+                           rope_tables)
     from .kernel_cache import get_or_compile
     check_qkv(Q, K, V)
     for t in (Q, K, V):
@@ -62,8 +64,10 @@ def prepare_attention(graph: Graph, Q, K, V, *, bias=None, cos=None, sin=None,
     args = N.FwdArgsC()
     fill_fwd_args(args, bundle.key.abi_tuple(), Q, K, V, out, save_lse, c, s,
                   slopes, b, None, bundle.sm_scale, bundle.window)
-    keep = (Q, K, V, out, save_lse, c, s, slopes, b)
-    return PreparedLaunch(N.lib().af_fwd, args, keep, Q.device), out
+    ws = fwd_workspace(args, Q.device)
+    keep = (Q, K, V, out, save_lse, c, s, slopes, b, ws)
+    return PreparedLaunch(N.lib().af_fwd, args, keep, Q.device,
+                          extra=(N.ptr(ws), _nbytes(ws))), out
 
 
 def prepare_decode(graph: Graph, Q, K, V, *, out=None, num_splits: int = 0,

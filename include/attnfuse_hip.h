@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define AF_ABI_VERSION 2
+#define AF_ABI_VERSION 3
 
 typedef enum af_status {
   AF_OK = 0,
@@ -114,7 +114,14 @@ typedef struct af_fwd_args {
   int32_t window;      /* sliding window size (AF_MASK_SLIDING_WINDOW)     */
 } af_fwd_args;
 
-int af_fwd(const af_fwd_args* args, void* stream);
+/* Workspace bytes af_fwd / af_fwd_blocksparse need for these arguments:
+ * with fused RoPE, the rotated keys k~ (B, H_kv, N_kv, D) in the input dtype,
+ * written once per call so that the attention kernel streams k~ instead of
+ * re-rotating every key tile in every query block; 0 without RoPE (the
+ * workspace may then be NULL). */
+size_t af_fwd_workspace_bytes(const af_fwd_args* args);
+int af_fwd(const af_fwd_args* args, void* workspace, size_t workspace_bytes,
+           void* stream);
 
 /* Block-sparse forward.  Replaces attnfuse_blocksparse_fwd_kernel
  * (reference: attnfuse/runtime/block_mask.py:205-271,
@@ -122,7 +129,7 @@ int af_fwd(const af_fwd_args* args, void* stream);
  * AF_MASK_BLOCK_SPARSE; the tile visited per listed block is whole (no
  * element mask inside it, reference semantics). */
 int af_fwd_blocksparse(const af_fwd_args* args, const af_blockmask* bm,
-                       void* stream);
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* Flash-decoding (one query row per head, split-K over the cache, then a
  * log-sum-exp combine).  Replaces attnfuse_decode_split_kernel +

@@ -23,7 +23,7 @@ def _declared_functions():
 
 def test_library_loads_and_reports_abi():
     lib = N.lib()
-    assert lib.af_abi_version() == 2
+    assert lib.af_abi_version() == 3
 
 
 def test_every_declared_symbol_is_exported():
@@ -80,31 +80,48 @@ def test_argument_errors_need_no_gpu():
     a.batch, a.heads_q, a.heads_kv, a.seqlen_q, a.seqlen_kv = 1, 4, 4, 64, 64
     for s in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
         s[:] = (64 * 4 * 64, 64 * 64, 64, 1)
-    assert lib.af_fwd(a, None) == N.AF_ERR_BAD_ARG
+    assert lib.af_fwd(a, None, 0, None) == N.AF_ERR_BAD_ARG
     assert "NULL" in N.last_error()
     # tensors with no rows are never touched and may be NULL: an empty
     # problem is accepted and returns before any launch
     a.seqlen_q = a.seqlen_kv = 0
-    assert lib.af_fwd(a, None) == N.AF_OK
+    assert lib.af_fwd(a, None, 0, None) == N.AF_OK
     a.seqlen_q = a.seqlen_kv = 64
-    assert lib.af_fwd(None, None) == N.AF_ERR_BAD_ARG
+    assert lib.af_fwd(None, None, 0, None) == N.AF_ERR_BAD_ARG
     # misaligned / non-unit strides are refused before any launch
     a.q = a.k = a.v = a.o = 16
     for s in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
         s[:] = (64 * 4 * 64, 64 * 64, 64, 2)
     a.batch, a.heads_q, a.heads_kv, a.seqlen_q, a.seqlen_kv = 1, 4, 4, 64, 64
-    assert lib.af_fwd(a, None) == N.AF_ERR_BAD_ARG
+    assert lib.af_fwd(a, None, 0, None) == N.AF_ERR_BAD_ARG
     assert "stride" in N.last_error()
     for s in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
         s[:] = (64 * 4 * 64, 64 * 64, 64, 1)
     a.heads_kv = 3
-    assert lib.af_fwd(a, None) == N.AF_ERR_BAD_ARG
+    assert lib.af_fwd(a, None, 0, None) == N.AF_ERR_BAD_ARG
     assert "multiple" in N.last_error()
     a.heads_kv = 4
     a.seqlen_kv = 32
-    assert lib.af_fwd(a, None) == N.AF_ERR_BAD_ARG        # causal needs Nq == Nkv
+    assert lib.af_fwd(a, None, 0, None) == N.AF_ERR_BAD_ARG        # causal needs Nq == Nkv
     a.key = N.SpecKeyC(2, 64, 0, 0, 0, 0)
-    assert lib.af_fwd(a, None) == N.AF_ERR_UNSUPPORTED
+    assert lib.af_fwd(a, None, 0, None) == N.AF_ERR_UNSUPPORTED
+    # fused RoPE needs the rotated-key workspace: B*Hkv*Nkv*D*2 bytes, rounded
+    # up to 256; refused before any launch when it is missing or too small
+    a.key = N.SpecKeyC(0, 64, 0, 0, 0, 1)
+    a.seqlen_kv = 64
+    a.cos = a.sin = 256
+    a.rope_stride[:] = (64, 1)
+    a.rope_len = 64
+    a.scale = 0.125
+    assert lib.af_fwd_workspace_bytes(a) == 1 * 4 * 64 * 64 * 2
+    a.seqlen_kv = a.seqlen_q = 63
+    assert lib.af_fwd_workspace_bytes(a) == (4 * 63 * 64 * 2 + 255) // 256 * 256
+    assert lib.af_fwd(a, None, 0, None) == N.AF_ERR_WORKSPACE
+    assert "workspace" in N.last_error()
+    assert lib.af_fwd(a, 256, 100, None) == N.AF_ERR_WORKSPACE
+    a.key = N.SpecKeyC(0, 64, 0, 0, 0, 0)
+    assert lib.af_fwd_workspace_bytes(a) == 0
+    assert lib.af_fwd_workspace_bytes(None) == 0
     with pytest.raises(NotImplementedError):
         N.check(N.AF_ERR_UNSUPPORTED)
     with pytest.raises(ValueError):
