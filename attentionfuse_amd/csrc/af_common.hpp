@@ -51,6 +51,10 @@ struct F16 {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(
         __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
+  // c + a.lo * b.lo + a.hi * b.hi (v_dot2c_f32_f16, fp32 accumulate)
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+  }
 };
 
 struct BF16 {
@@ -79,6 +83,11 @@ struct BF16 {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
         __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
         0);
+  }
+  // c + a.lo * b.lo + a.hi * b.hi (v_dot2c_f32_bf16, fp32 accumulate)
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                           false);
   }
 };
 
@@ -331,6 +340,36 @@ struct TileDma {
       const int m = w + i * WAVES;   // wave-uniform
       if (INSTR % WAVES != 0 && m >= INSTR) break;
       buf_ld16_lds(64 * m >= CHUNKS ? br : ar, lds + stage + 512 * m, off[i]);
+    }
+  }
+};
+
+// One tensor's rows [r0, r0 + ROWS) into a swizzled LDS tile, the same way.
+template <int D, int NT, int ROWS>
+struct RowsDma {
+  static_assert(ROWS % 16 == 0 && ROWS * D % 512 == 0, "whole wave instructions per tile");
+  static constexpr int CHUNKS = ROWS * D / 8;
+  static constexpr int INSTR = CHUNKS / 64;
+  static constexpr int WAVES = NT / 64;
+  static constexpr int IPW = (INSTR + WAVES - 1) / WAVES;
+  uint32_t off[IPW];
+
+  __device__ void init(int w, int lane, int64_t stride) {
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int pos = 64 * (w + i * WAVES) + lane;
+      const int row = pos / (D / 8), kp = pos % (D / 8);
+      off[i] = (uint32_t)((row * stride + 8 * (kp ^ lds_swz<D>(row))) * 2);
+    }
+  }
+  // tile = element offset of the tile inside `lds`
+  __device__ void load(uint16_t* lds, int tile, int w, const uint16_t* base, int64_t stride, int n, int r0) const {
+    const auto rs = make_rsrc(base + (int64_t)r0 * stride, span_bytes<D>(n - r0, stride));
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int m = w + i * WAVES;   // wave-uniform
+      if (INSTR % WAVES != 0 && m >= INSTR) break;
+      buf_ld16_lds(rs, lds + tile + 512 * m, off[i]);
     }
   }
 };

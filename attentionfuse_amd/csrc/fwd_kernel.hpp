@@ -72,9 +72,9 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   constexpr int KS = D / 16;         // 16-deep k-steps of Q K^T
   constexpr int DB = D / 32;         // 32-row blocks of O^T
   constexpr int TILE = BN * D;       // one swizzled (BN x D) tile, no padding
-  constexpr int STAGE = 2 * TILE;    // K tile, then V tile
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+  // two K slots, then two V slots
+  __shared__ __attribute__((aligned(16))) uint16_t lds[4 * TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -162,15 +162,16 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     }
   };
 
-  // ---- K / V staging: buffer loads straight into the swizzled LDS stage ----
+  // ---- K / V staging: buffer loads straight into swizzled LDS tiles ----------
   // Rows past N_kv fall outside the buffer resources and load as zeros (their
   // scores are masked anyway).  With RoPE the K given here is already
-  // rotated (k~, written once per key by rope_rows_kernel).
-  TileDma<D, NT, BN> dma;
-  dma.init(w, lane, kstr, vstr);
-  auto stage_load = [&](int t) {
-    dma.load(lds, (t & 1) * STAGE, w, kbase, kstr, p.Nkv, vbase, vstr, p.Nkv, tile_n0(t));
-  };
+  // rotated (k~, written once per key by rope_rows_kernel).  Two K slots and
+  // two V slots: K runs one tile ahead of V (see the pipeline below).
+  RowsDma<D, NT, BN> kdma, vdma;
+  kdma.init(w, lane, kstr);
+  vdma.init(w, lane, vstr);
+  auto load_k = [&](int t) { kdma.load(lds, (t & 1) * TILE, w, kbase, kstr, p.Nkv, tile_n0(t)); };
+  auto load_v = [&](int t) { vdma.load(lds, (2 + (t & 1)) * TILE, w, vbase, vstr, p.Nkv, tile_n0(t)); };
   // per-lane LDS offsets: the K rows of the S^T MFMA (key block 0; block 1 is
   // 32 rows on, same swizzle) and the transposed V reads of the P V MFMA
   int koff[KS];
@@ -188,21 +189,15 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // moves when a new score exceeds it by more than kTau, so P = 2^(x - m)
   // stays <= 2^kTau (exact in fp16/bf16 up to rounding) and the O rescale
   // (a multiply of every accumulator) is skipped on almost every tile.  Row
-  // sums come out of the MFMA pipe: an all-ones A operand times P^T gives
-  // sum_k P[k][q] in every row of a 32x32 block.
+  // sums are v_dot2 of the packed P with (1, 1).
   constexpr float kTau = 8.f;
   constexpr float kNegBig = -1.0e30f;
   f32x16 o[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) o[db] = f32x16{};
-  f32x16 lacc = f32x16{};
+  float lsum[2] = {0.f, 0.f};
   float m_run = kNegBig;
-  // Materialised once through an opaque move: left as a constant the
-  // compiler re-creates it every iteration in registers that collide with
-  // the O accumulators and then has to copy O around the MFMA chain.
-  uint32_t one_pair;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(one_pair) : "s"(E::kOnePair));
-  const u32x4 ones = {one_pair, one_pair, one_pair, one_pair};
+  const uint32_t one_pair = E::kOnePair;
   float slope2 = 0.f;
   if constexpr (BIAS == BIAS_ALIBI) slope2 = p.slopes[hq] * kLog2e;
   // Causal-type masks: every visible key has j <= i, so -slope |i - j| =
@@ -212,17 +207,21 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   const uint16_t* brow = nullptr;
   if constexpr (BIAS == BIAS_ADD) brow = p.bias + b * p.bs[0] + hq * p.bs[1] + (int64_t)qrow * p.bs[2];
 
-  if (ntiles > 0) stage_load(0);
-  wait_lds_dma();
-  __syncthreads();
+  // S^T = K Q^T of tile t (two 32-key blocks), K from its LDS slot.
+  auto scores = [&](int t, f32x16* s) {
+    const uint16_t* Ks = lds + (t & 1) * TILE;
+#pragma unroll
+    for (int kb = 0; kb < BN / 32; ++kb) {
+      s[kb] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) s[kb] = E::mfma32(ld16(Ks + 32 * kb * D + koff[ks]), qf[ks], s[kb]);
+    }
+  };
 
-  for (int t = 0; t < ntiles; ++t) {
+  // Mask, bias and softmax of tile t's scores s, then O += P V(t).
+  auto softmax_pv = [&](int t, f32x16* s) {
     const int n0 = tile_n0(t);
-    const bool more = t + 1 < ntiles;
-    if (more) stage_load(t + 1);
-    const uint16_t* Ks = lds + (t & 1) * STAGE;
-    const uint16_t* Vs = Ks + TILE;
-
+    const uint16_t* Vs = lds + (2 + (t & 1)) * TILE;
     bool active = q0w < p.Nq && n0 >= 0 && n0 < p.Nkv;
     if constexpr (MASK == MASK_CAUSAL) active = active && n0 <= q0w + 31;
     if constexpr (MASK == MASK_SW)
@@ -238,16 +237,6 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
       atomicAdd(p.coverage + ci, 1u);
     }
     {
-      // S^T = K Q^T over this stage: two 32-key blocks.
-      f32x16 s[BN / 32];
-#pragma unroll
-      for (int kb = 0; kb < BN / 32; ++kb) {
-        s[kb] = f32x16{};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          s[kb] = E::mfma32(ld16(Ks + 32 * kb * D + koff[ks]), qf[ks], s[kb]);
-      }
-
       bool need_mask = !active || n0 + BN > p.Nkv;
       if constexpr (MASK == MASK_CAUSAL) need_mask = need_mask || n0 + BN - 1 > q0w;
       if constexpr (MASK == MASK_SW)
@@ -348,12 +337,8 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
               asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x) : "v"(alpha));
               o[db][r] = x;
             }
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float x = lacc[r];
-            asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x) : "v"(alpha));
-            lacc[r] = x;
-          }
+          lsum[0] *= alpha;
+          lsum[1] *= alpha;
           asm volatile("s_nop 7");
           m_run = m_new;
         }
@@ -378,8 +363,12 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
         for (int i = 0; i < 4; ++i)
           pf[kk][i] = E::pack(s[kb][8 * j + 2 * i], s[kb][8 * j + 2 * i + 1]);
       }
+      // row sums of the rounded P (this lane's 32 keys; the partner lane
+      // l ^ 32 holds the other 32), fp32 accumulation, two chains
 #pragma unroll
-      for (int kk = 0; kk < BN / 16; ++kk) lacc = E::mfma32(ones, pf[kk], lacc);
+      for (int kk = 0; kk < BN / 16; ++kk)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lsum[kk & 1] = E::dot2(pf[kk][i], one_pair, lsum[kk & 1]);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
 #pragma unroll
@@ -393,15 +382,45 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
       }
     }
 
-    // this wave's loads of stage t+1 have landed; after the barrier every
-    // wave's have, and no wave reads stage t any more
+  };
+
+  // ---- software pipeline ---------------------------------------------------
+  // Iteration t issues the loads of K(t+2) and V(t+1), the score MFMAs of
+  // tile t+1 (they run on the matrix pipe while this wave does the softmax
+  // of tile t on the VALU), then softmax(t) and P V(t).  Slot reuse: K(t+2)
+  // overwrites K(t), last read by the score MFMAs of iteration t-1; V(t+1)
+  // overwrites V(t-1), last read in iteration t-1; the barrier closing each
+  // iteration separates the two.
+  if (ntiles > 0) {
+    load_k(0);
+    load_v(0);
+  }
+  if (ntiles > 1) load_k(1);
+  wait_lds_dma();
+  __syncthreads();
+  f32x16 sa[BN / 32], sb[BN / 32];
+  if (ntiles > 0) scores(0, sa);
+  auto step = [&](int t, f32x16* cur, f32x16* nxt) {
+    if (t + 2 < ntiles) load_k(t + 2);
+    if (t + 1 < ntiles) {
+      load_v(t + 1);
+      scores(t + 1, nxt);
+    }
+    softmax_pv(t, cur);
+    // this wave's loads have landed; after the barrier every wave's have,
+    // and no wave reads slot K(t) / V(t) any more
     wait_lds_dma();
     __syncthreads();
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    step(t, sa, sb);
+    if (t + 1 < ntiles) step(t + 1, sb, sa);
   }
 
   // ---- epilogue -------------------------------------------------------------
-  // every register of lacc holds this lane's query row sum
-  const float lt = lacc[0];
+  // this lane's 32 keys of every tile, plus the partner lane's 32
+  float lt = lsum[0] + lsum[1];
+  lt += xor32(lt);
   const float inv = (lt == 0.f) ? 1.f : 1.f / lt;
   if (qrow < p.Nq) {
     uint16_t* orow = p.o + b * p.os[0] + hq * p.os[1] + (int64_t)qrow * p.os[2];
