@@ -218,10 +218,14 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     }
   };
 
-  // Mask, bias and softmax of tile t's scores s, then O += P V(t).
-  auto softmax_pv = [&](int t, f32x16* s) {
+  // Bias, mask and running max of tile t's scores s (with the rare O
+  // rescale); returns the affine map (zc, off) from a score to its logit
+  // minus the running max.
+  struct Logit {
+    float zc, off;
+  };
+  auto prepare = [&](int t, f32x16* s) -> Logit {
     const int n0 = tile_n0(t);
-    const uint16_t* Vs = lds + (2 + (t & 1)) * TILE;
     bool active = q0w < p.Nq && n0 >= 0 && n0 < p.Nkv;
     if constexpr (MASK == MASK_CAUSAL) active = active && n0 <= q0w + 31;
     if constexpr (MASK == MASK_SW)
@@ -342,55 +346,61 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
           asm volatile("s_nop 7");
           m_run = m_new;
         }
-        const float off = zoff - m_run;
-#pragma unroll
-        for (int kb = 0; kb < BN / 32; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[kb][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], zc, off));
+        return Logit{zc, zoff - m_run};
       } else {
-#pragma unroll
-        for (int kb = 0; kb < BN / 32; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[kb][r] = fmaxf(__builtin_fmaf(s[kb][r], zc, zoff), 0.f);
-      }
-
-      // P^T (registers) -> B operands, one per 16 keys.
-      u32x4 pf[BN / 16];
-#pragma unroll
-      for (int kk = 0; kk < BN / 16; ++kk) {
-        const int kb = kk >> 1, j = kk & 1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          pf[kk][i] = E::pack(s[kb][8 * j + 2 * i], s[kb][8 * j + 2 * i + 1]);
-      }
-      // row sums of the rounded P (this lane's 32 keys; the partner lane
-      // l ^ 32 holds the other 32), fp32 accumulation, two chains
-#pragma unroll
-      for (int kk = 0; kk < BN / 16; ++kk)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) lsum[kk & 1] = E::dot2(pf[kk][i], one_pair, lsum[kk & 1]);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-#pragma unroll
-        for (int kk = 0; kk < BN / 16; ++kk) {
-          const uint16_t* vt = Vs + 16 * kk * D;
-          const u32x2 lo = lds_read_tr16(vt + voff[db][0]);
-          const u32x2 hi = lds_read_tr16(vt + voff[db][1]);
-          const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
-          o[db] = E::mfma32(va, pf[kk], o[db]);
-        }
+        return Logit{zc, zoff};
       }
     }
+  };
 
+  // The straight-line body of one pipeline step, one basic block: the score
+  // MFMAs of tile t+1 into nxt, P = 2^(logit) (or relu) of tile t with its
+  // row sums, and O += P V(t).
+  auto exp_pv = [&](int t, f32x16* s, f32x16* nxt, Logit lg) {
+    scores(t + 1, nxt);
+    const uint16_t* Vs = lds + (2 + (t & 1)) * TILE;
+#pragma unroll
+    for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float x = __builtin_fmaf(s[kb][r], lg.zc, lg.off);
+        s[kb][r] = (NORM == NORM_SOFTMAX) ? __builtin_amdgcn_exp2f(x) : fmaxf(x, 0.f);
+      }
+    // P^T (registers) -> B operands, one per 16 keys.
+    u32x4 pf[BN / 16];
+#pragma unroll
+    for (int kk = 0; kk < BN / 16; ++kk) {
+      const int kb = kk >> 1, j = kk & 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pf[kk][i] = E::pack(s[kb][8 * j + 2 * i], s[kb][8 * j + 2 * i + 1]);
+    }
+    // row sums of the rounded P (this lane's 32 keys; the partner lane
+    // l ^ 32 holds the other 32), fp32 accumulation, two chains
+#pragma unroll
+    for (int kk = 0; kk < BN / 16; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lsum[kk & 1] = E::dot2(pf[kk][i], one_pair, lsum[kk & 1]);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int kk = 0; kk < BN / 16; ++kk) {
+        const uint16_t* vt = Vs + 16 * kk * D;
+        const u32x2 lo = lds_read_tr16(vt + voff[db][0]);
+        const u32x2 hi = lds_read_tr16(vt + voff[db][1]);
+        const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
+        o[db] = E::mfma32(va, pf[kk], o[db]);
+      }
+    }
   };
 
   // ---- software pipeline ---------------------------------------------------
-  // Iteration t issues the loads of K(t+2) and V(t+1), the score MFMAs of
-  // tile t+1 (they run on the matrix pipe while this wave does the softmax
-  // of tile t on the VALU), then softmax(t) and P V(t).  Slot reuse: K(t+2)
-  // overwrites K(t), last read by the score MFMAs of iteration t-1; V(t+1)
-  // overwrites V(t-1), last read in iteration t-1; the barrier closing each
-  // iteration separates the two.
+  // Iteration t issues the loads of K(t+2) and V(t+1), masks tile t and
+  // updates the running max, then runs the score MFMAs of tile t+1 (on the
+  // matrix pipe while this wave computes P of tile t on the VALU) and
+  // P V(t).  In the last iteration the score MFMAs read a stale K slot and
+  // their result is dropped.  Slot reuse: K(t+2) overwrites K(t), last read
+  // by the score MFMAs of iteration t-1; V(t+1) overwrites V(t-1), last read
+  // in iteration t-1; the barrier closing each iteration separates the two.
   if (ntiles > 0) {
     load_k(0);
     load_v(0);
@@ -402,11 +412,8 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   if (ntiles > 0) scores(0, sa);
   auto step = [&](int t, f32x16* cur, f32x16* nxt) {
     if (t + 2 < ntiles) load_k(t + 2);
-    if (t + 1 < ntiles) {
-      load_v(t + 1);
-      scores(t + 1, nxt);
-    }
-    softmax_pv(t, cur);
+    if (t + 1 < ntiles) load_v(t + 1);
+    exp_pv(t, cur, nxt, prepare(t, cur));
     // this wave's loads have landed; after the barrier every wave's have,
     // and no wave reads slot K(t) / V(t) any more
     wait_lds_dma();
