@@ -29,7 +29,6 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 struct F16 {
   using T = _Float16;
   using V8 = f16x8;
-  static constexpr uint32_t kOnePair = 0x3c003c00u;   // (1.0, 1.0)
   __device__ static inline float lo(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
   }
@@ -51,16 +50,16 @@ struct F16 {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(
         __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
-  // c + a.lo * b.lo + a.hi * b.hi (v_dot2c_f32_f16, fp32 accumulate)
-  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+  // lo += w.lo, hi += w.hi in fp32 (v_fma_mix_f32 reads the f16 halves)
+  __device__ static inline void add_pair(uint32_t w, float& lo, float& hi) {
+    asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]" : "+v"(lo) : "v"(w));
+    asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(hi) : "v"(w));
   }
 };
 
 struct BF16 {
   using T = __bf16;
   using V8 = bf16x8;
-  static constexpr uint32_t kOnePair = 0x3f803f80u;   // (1.0, 1.0)
   __device__ static inline float lo(uint32_t w) {
     return __builtin_bit_cast(float, w << 16);
   }
@@ -84,10 +83,10 @@ struct BF16 {
         __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
         0);
   }
-  // c + a.lo * b.lo + a.hi * b.hi (v_dot2c_f32_bf16, fp32 accumulate)
-  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
-                                           false);
+  // lo += w.lo, hi += w.hi in fp32 (a bf16 is the top half of its fp32)
+  __device__ static inline void add_pair(uint32_t w, float& lo, float& hi) {
+    lo += __builtin_bit_cast(float, w << 16);
+    hi += __builtin_bit_cast(float, w & 0xffff0000u);
   }
 };
 

@@ -189,7 +189,12 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // moves when a new score exceeds it by more than kTau, so P = 2^(x - m)
   // stays <= 2^kTau (exact in fp16/bf16 up to rounding) and the O rescale
   // (a multiply of every accumulator) is skipped on almost every tile.  Row
-  // sums are v_dot2 of the packed P with (1, 1).
+  // sums add the rounded P that the P V MFMA uses, in fp32, so O = sum P V /
+  // sum P stays a weighted mean of V even for one dominant key (the reference
+  // sums the unrounded p, attnfuse/compiler/codegen.py:227, which is further
+  // from exact attention).  v_fma_mix (f16) or shift/mask + add (bf16)
+  // overlap with the MFMAs of other waves; v_dot2 on the packed P and
+  // all-ones MFMAs were measured to serialise with them.
   constexpr float kTau = 8.f;
   constexpr float kNegBig = -1.0e30f;
   f32x16 o[DB];
@@ -197,7 +202,6 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   for (int db = 0; db < DB; ++db) o[db] = f32x16{};
   float lsum[2] = {0.f, 0.f};
   float m_run = kNegBig;
-  const uint32_t one_pair = E::kOnePair;
   float slope2 = 0.f;
   if constexpr (BIAS == BIAS_ALIBI) slope2 = p.slopes[hq] * kLog2e;
   // Causal-type masks: every visible key has j <= i, so -slope |i - j| =
@@ -375,11 +379,11 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
       for (int i = 0; i < 4; ++i) pf[kk][i] = E::pack(s[kb][8 * j + 2 * i], s[kb][8 * j + 2 * i + 1]);
     }
     // row sums of the rounded P (this lane's 32 keys; the partner lane
-    // l ^ 32 holds the other 32), fp32 accumulation, two chains
+    // l ^ 32 holds the other 32), fp32, two chains
 #pragma unroll
     for (int kk = 0; kk < BN / 16; ++kk)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) lsum[kk & 1] = E::dot2(pf[kk][i], one_pair, lsum[kk & 1]);
+      for (int i = 0; i < 4; ++i) E::add_pair(pf[kk][i], lsum[0], lsum[1]);
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
