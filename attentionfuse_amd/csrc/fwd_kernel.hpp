@@ -61,10 +61,19 @@ struct FwdParams {
   int32_t window;
 };
 
+// Waves per SIMD the register budget is set for: head dims up to 64 fit
+// 168 VGPRs (three waves), except causal-type ALiBi, whose initial score
+// accumulator takes 16 more (two waves); D = 128 takes one.
+template <int D, int MASK, int BIAS>
+constexpr int fwd_waves_per_eu() {
+  if (D > 64) return 1;
+  return (BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW)) ? 2 : 3;
+}
+
 // Head dims up to 64 fit in 168 VGPRs (a few setup values spill outside the
 // loop): three waves per SIMD, three 4-wave workgroups per CU.
 template <class E, int D, int MASK, int BIAS, int NORM, bool ROPE, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 1)))
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(fwd_waves_per_eu<D, MASK, BIAS>())))
     fwd_kernel(const FwdParams p) {
   constexpr int NT = WAVES * 64;
   constexpr int BM = 32 * WAVES;
@@ -205,9 +214,20 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   float slope2 = 0.f;
   if constexpr (BIAS == BIAS_ALIBI) slope2 = p.slopes[hq] * kLog2e;
   // Causal-type masks: every visible key has j <= i, so -slope |i - j| =
-  // slope (j - i), linear in the key index: accumulated with one add per
-  // score while walking the lane's keys in order.
+  // slope (j - i) is linear in the key index.  Register r of a 32-key block
+  // holds key j0 + k_r (j0 = block start + 8h, k_r = 16 (r/8) + r%8), so the
+  // logit is (s + u k_r) * zc + slope (j0 - i) with u = slope / zc: the
+  // u k_r part is the initial accumulator of the score MFMAs (the same for
+  // every tile and lane) and slope (j0 - i) is one offset per block.
   constexpr bool kAlibiOneSided = BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW);
+  const float zc0 = (NORM == NORM_SOFTMAX) ? c2 : p.scale;            // score -> logit scale
+  const float aslope = (NORM == NORM_SOFTMAX) ? slope2 : slope2 * kLn2;  // slope in logit units
+  f32x16 sinit = f32x16{};
+  if constexpr (kAlibiOneSided) {
+    const float u = aslope / zc0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sinit[r] = u * (float)(16 * (r >> 3) + (r & 7));
+  }
   const uint16_t* brow = nullptr;
   if constexpr (BIAS == BIAS_ADD) brow = p.bias + b * p.bs[0] + hq * p.bs[1] + (int64_t)qrow * p.bs[2];
 
@@ -216,7 +236,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     const uint16_t* Ks = lds + (t & 1) * TILE;
 #pragma unroll
     for (int kb = 0; kb < BN / 32; ++kb) {
-      s[kb] = f32x16{};
+      s[kb] = sinit;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) s[kb] = E::mfma32(ld16(Ks + 32 * kb * D + koff[ks]), qf[ks], s[kb]);
     }
@@ -226,7 +246,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // rescale); returns the affine map (zc, off) from a score to its logit
   // minus the running max.
   struct Logit {
-    float zc, off;
+    float zc, off[BN / 32];
   };
   auto prepare = [&](int t, f32x16* s) -> Logit {
     const int n0 = tile_n0(t);
@@ -252,10 +272,13 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
       if constexpr (MASK == MASK_CSW)
         need_mask = need_mask || (q0w + 31 - n0 >= p.window) || n0 + BN - 1 > q0w;
 
-      // Logit of element r: s[r] * zc + zoff (log2 units for softmax,
-      // natural units for relu).
-      float zc = (NORM == NORM_SOFTMAX) ? c2 : p.scale;
-      const float zoff = 0.f;
+      // Logit of element r of key block kb: s[r] * zc + zoff[kb] (log2 units
+      // for softmax, natural units for relu).
+      float zc = zc0;
+      float zoff[BN / 32];
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb)
+        zoff[kb] = kAlibiOneSided ? aslope * (float)(n0 + 32 * kb + 8 * h - qrow) : 0.f;
       if constexpr (BIAS == BIAS_ADD) {
         const float bscale = (NORM == NORM_SOFTMAX) ? kLog2e : 1.f;
 #pragma unroll
@@ -278,30 +301,17 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
           }
         zc = 1.f;
       } else if constexpr (BIAS == BIAS_ALIBI) {
-        const float sl = (NORM == NORM_SOFTMAX) ? slope2 : slope2 * kLn2;
-        if constexpr (kAlibiOneSided) {
-          // keys of register r: n0 + 32 kb + 16 (r/8) + 8h + (r%8)
-#pragma unroll
-          for (int kb = 0; kb < BN / 32; ++kb)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              float bias = sl * (float)(n0 + 32 * kb + 16 * j + 8 * h - qrow);
-#pragma unroll
-              for (int e = 0; e < 8; ++e) {
-                s[kb][8 * j + e] = __builtin_fmaf(s[kb][8 * j + e], zc, bias);
-                bias += sl;
-              }
-            }
-        } else {
+        if constexpr (!kAlibiOneSided) {
+          // two-sided windows: -slope |i - j| per element
 #pragma unroll
           for (int kb = 0; kb < BN / 32; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int key = n0 + 32 * kb + acc_key(r, h);
-              s[kb][r] = __builtin_fmaf(s[kb][r], zc, -sl * (float)abs(qrow - key));
+              s[kb][r] = __builtin_fmaf(s[kb][r], zc, -aslope * (float)abs(qrow - key));
             }
+          zc = 1.f;
         }
-        zc = 1.f;
       }
       if (need_mask) {
 #pragma unroll
@@ -319,11 +329,22 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
 
       if constexpr (NORM == NORM_SOFTMAX) {
         float mz = -INFINITY;
+        if constexpr (kAlibiOneSided) {
 #pragma unroll
-        for (int kb = 0; kb < BN / 32; ++kb)
+          for (int kb = 0; kb < BN / 32; ++kb) {
+            float mk = -INFINITY;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mz = fmaxf(mz, s[kb][r]);
-        const float mx = max_xor32(__builtin_fmaf(mz, zc, zoff));
+            for (int r = 0; r < 16; ++r) mk = fmaxf(mk, s[kb][r]);
+            mz = fmaxf(mz, __builtin_fmaf(mk, zc, zoff[kb]));
+          }
+        } else {
+#pragma unroll
+          for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mz = fmaxf(mz, s[kb][r]);
+          mz = __builtin_fmaf(mz, zc, zoff[0]);
+        }
+        const float mx = max_xor32(mz);
         // The rescale runs only when some row of the wave grew past the
         // slack.  It multiplies the accumulators in place (tied asm
         // operands): written as plain C++ inside the branch, the register
@@ -350,9 +371,17 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
           asm volatile("s_nop 7");
           m_run = m_new;
         }
-        return Logit{zc, zoff - m_run};
+        Logit lg;
+        lg.zc = zc;
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb) lg.off[kb] = zoff[kb] - m_run;
+        return lg;
       } else {
-        return Logit{zc, zoff};
+        Logit lg;
+        lg.zc = zc;
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb) lg.off[kb] = zoff[kb];
+        return lg;
       }
     }
   };
@@ -367,7 +396,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     for (int kb = 0; kb < BN / 32; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float x = __builtin_fmaf(s[kb][r], lg.zc, lg.off);
+        const float x = __builtin_fmaf(s[kb][r], lg.zc, lg.off[kb]);
         s[kb][r] = (NORM == NORM_SOFTMAX) ? __builtin_amdgcn_exp2f(x) : fmaxf(x, 0.f);
       }
     // P^T (registers) -> B operands, one per 16 keys.
