@@ -10,9 +10,18 @@
 
 namespace af {
 
+int bwd_group_split(const af_bwd_args& a) {
+  if (a.batch <= 0 || a.heads_kv <= 0 || a.heads_q <= 0 || a.seqlen_kv <= 0 || a.heads_q % a.heads_kv != 0) return 1;
+  const int G = a.heads_q / a.heads_kv;
+  const int64_t base = (int64_t)((a.seqlen_kv + 127) / 128) * a.batch * a.heads_kv;
+  int gs = 1;
+  while (G % (2 * gs) == 0 && base * 2 * gs <= 512) gs *= 2;
+  return gs;
+}
+
 BwdWorkspace bwd_workspace_layout(const af_bwd_args& a) {
   auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
-  BwdWorkspace w{0, 0, 0, 0};
+  BwdWorkspace w{0, 0, 0, 0, 0, 0, 1};
   if (a.batch <= 0 || a.heads_q <= 0 || a.heads_kv <= 0 || a.seqlen_q < 0 || a.seqlen_kv < 0 || a.key.head_dim <= 0)
     return w;
   const size_t rows_q = (size_t)a.batch * a.heads_q * a.seqlen_q;
@@ -24,6 +33,13 @@ BwdWorkspace bwd_workspace_layout(const af_bwd_args& a) {
     w.total += up(rows_q * a.key.head_dim * 2);
     w.kr = w.total;
     w.total += up(rows_k * a.key.head_dim * 2);
+  }
+  w.g_split = bwd_group_split(a);
+  if (w.g_split > 1) {
+    w.dkp = w.total;
+    w.total += up((size_t)w.g_split * rows_k * a.key.head_dim * 4);
+    w.dvp = w.total;
+    w.total += up((size_t)w.g_split * rows_k * a.key.head_dim * 4);
   }
   if (rows_q == 0 && rows_k == 0) w.total = 0;
   return w;
@@ -100,6 +116,11 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   if (k.rope) {
     p.qr = reinterpret_cast<uint16_t*>(ws + wl.qr);
     p.kr = reinterpret_cast<uint16_t*>(ws + wl.kr);
+  }
+  p.g_split = wl.g_split;
+  if (wl.g_split > 1) {
+    p.dkp = reinterpret_cast<float*>(ws + wl.dkp);
+    p.dvp = reinterpret_cast<float*>(ws + wl.dvp);
   }
   p.dq = static_cast<uint16_t*>(a->dq);
   p.dk = static_cast<uint16_t*>(a->dk);
@@ -184,8 +205,13 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
                        (k.rope ? (int64_t)a->batch * a->heads_kv * a->seqlen_kv : 0);
   const int rpb = 256 / (k.head_dim / 16);
   g.prep = (unsigned)std::max<int64_t>(1, (rows + rpb - 1) / rpb);
-  g.dkv = (unsigned)std::max(1, p.n_kblocks * a->batch * a->heads_kv);
+  g.dkv = (unsigned)std::max(1, p.n_kblocks * p.g_split * a->batch * a->heads_kv);
   g.dq = (unsigned)std::max(1, p.n_qblocks * a->batch * a->heads_q);
+  g.combine = 0;
+  if (p.g_split > 1) {
+    const int64_t krows = (int64_t)a->batch * a->heads_kv * a->seqlen_kv;
+    g.combine = (unsigned)((krows + rpb - 1) / rpb);
+  }
 
   const bool f16 = k.dtype == AF_F16;
   int r = -1;

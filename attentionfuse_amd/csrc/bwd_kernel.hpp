@@ -77,6 +77,13 @@ struct BwdParams {
   int32_t bs_block_m, bs_block_n;
   int32_t n_qblocks, n_kblocks;   // workgroup tiling of the two kernels
   int32_t rope_len;               // rows of the RoPE tables
+  // dK/dV: the G query heads of a key/value head are split over g_split
+  // workgroups per key block; with g_split > 1 each writes fp32 partial sums
+  // (unscaled, rotated space) to dkp / dvp, (g_split, B, Hkv, Nkv, D), and
+  // bwd_dkv_combine_kernel adds them up.
+  int32_t g_split;
+  float* dkp;
+  float* dvp;
   float scale;
 };
 
@@ -191,6 +198,79 @@ __device__ inline void store_grad_rows(f32x16* acc, uint16_t* out, int64_t rstri
     }
 }
 
+// fp32 row of a transposed 32x32-block accumulator (rows = dims, column =
+// this lane's row): register 4g + e of block db is dim 32 db + 8 g + 4 h + e.
+template <int D>
+__device__ inline void store_partial_row(const f32x16* acc, float* out, int h) {
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * db + 8 * g + 4 * h;
+      *reinterpret_cast<f32x4*>(out + d0) =
+          f32x4{acc[db][4 * g], acc[db][4 * g + 1], acc[db][4 * g + 2], acc[db][4 * g + 3]};
+    }
+}
+
+// dK, dV of key row n = the sum of the g_split partial rows; dK is scaled and,
+// with RoPE, rotated back to the input space (the transpose of rotate-half).
+// Thread j of a row handles dims [8 j, 8 j + 8) and their rotate-half
+// partners [8 j + D/2, ...).
+template <class E, int D, bool ROPE>
+__global__ void __launch_bounds__(256) bwd_dkv_combine_kernel(const BwdParams p) {
+  constexpr int TPR = D / 16;
+  constexpr int RPB = 256 / TPR;
+  const int tid = threadIdx.x;
+  const int64_t r = (int64_t)blockIdx.x * RPB + tid / TPR;
+  const int64_t rows = (int64_t)p.B * p.Hkv * p.Nkv;
+  if (r >= rows) return;
+  const int j = tid % TPR;
+  const int n = (int)(r % p.Nkv);
+  const int64_t bh = r / p.Nkv;
+  const int hk = (int)(bh % p.Hkv), b = (int)(bh / p.Hkv);
+  const int dl = 8 * j, dh = dl + D / 2;
+  float vlo[8], vhi[8], klo[8], khi[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) vlo[e] = vhi[e] = klo[e] = khi[e] = 0.f;
+  for (int sp = 0; sp < p.g_split; ++sp) {
+    const int64_t off = (sp * rows + r) * D;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(p.dvp + off + dl + 4 * q);
+      const f32x4 c = *reinterpret_cast<const f32x4*>(p.dvp + off + dh + 4 * q);
+      const f32x4 x = *reinterpret_cast<const f32x4*>(p.dkp + off + dl + 4 * q);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(p.dkp + off + dh + 4 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vlo[4 * q + e] += a[e];
+        vhi[4 * q + e] += c[e];
+        klo[4 * q + e] += x[e];
+        khi[4 * q + e] += y[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    klo[e] *= p.scale;
+    khi[e] *= p.scale;
+  }
+  if constexpr (ROPE) {
+    float cl[8], sl[8], ch[8], sh[8];
+    unpack8<E>(ld16(p.cos + n * p.rs[0] + dl), cl);
+    unpack8<E>(ld16(p.sin + n * p.rs[0] + dl), sl);
+    unpack8<E>(ld16(p.cos + n * p.rs[0] + dh), ch);
+    unpack8<E>(ld16(p.sin + n * p.rs[0] + dh), sh);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) rope_grad_pair(klo[e], khi[e], cl[e], sl[e], ch[e], sh[e]);
+  }
+  uint16_t* dvrow = p.dv + b * p.dvs[0] + hk * p.dvs[1] + n * p.dvs[2];
+  uint16_t* dkrow = p.dk + b * p.dks[0] + hk * p.dks[1] + n * p.dks[2];
+  st16(dvrow + dl, pack8<E>(vlo));
+  st16(dvrow + dh, pack8<E>(vhi));
+  st16(dkrow + dl, pack8<E>(klo));
+  st16(dkrow + dh, pack8<E>(khi));
+}
+
 // Masking of one score element (query i, key j); the range logic of each
 // kernel decides which tiles are visited at all and which need this test.
 template <int MASK>
@@ -224,11 +304,16 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   // key block outermost: under a causal mask the first key blocks see the
-  // most query tiles, so they are dispatched first.
+  // most query tiles, so they are dispatched first.  Then the head-group
+  // split, then (batch, key/value head).
   const int BHK = p.B * p.Hkv;
-  const int kb = blockIdx.x / BHK;
-  const int bhk = blockIdx.x % BHK;
+  const int kb = blockIdx.x / (BHK * p.g_split);
+  const int rem = blockIdx.x - kb * (BHK * p.g_split);
+  const int split = rem / BHK;
+  const int bhk = rem - split * BHK;
   const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
+  const int gper = p.G / p.g_split;       // query heads of this workgroup
+  const int hq0 = hk * p.G + split * gper;
   const int n0 = kb * BK;
   const int n0w = n0 + 32 * w;
   const int key = n0w + c;
@@ -281,14 +366,14 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
       return m_lo + 32 * t;
     }
   };
-  const int ntiles = ntq * p.G;
+  const int ntiles = ntq * gper;
 
   TileDma<D, NT> dma;
   dma.init(w, lane, p.qts[2], p.dos[2]);
   float lreg = 0.f, dreg = 0.f;
   // issue the tile loads of stage t into LDS slot `slot`, and fetch its L / delta
   auto stage_load = [&](int t, int slot) {
-    const int gi = t / ntq, hq = hk * p.G + gi;
+    const int gi = t / ntq, hq = hq0 + gi;
     const int m0 = tile_m0(t - gi * ntq);
     dma.load(lds, slot * STAGE, w, p.qt + b * p.qts[0] + hq * p.qts[1], p.qts[2], p.Nq,
              p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], p.Nq, m0);
@@ -328,7 +413,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   for (int t = 0; t < ntiles; ++t) {
     const bool more = t + 1 < ntiles;
     if (more) stage_load(t + 1, (t + 1) & 1);
-    const int gi = t / ntq, hq = hk * p.G + gi;
+    const int gi = t / ntq, hq = hq0 + gi;
     const int m0 = tile_m0(t - gi * ntq);
     const uint16_t* buf = lds + (t & 1) * STAGE;
     const uint16_t* Qs = buf;
@@ -434,6 +519,14 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
 
   uint16_t* dkb = p.dk + b * p.dks[0] + hk * p.dks[1];
   uint16_t* dvb = p.dv + b * p.dvs[0] + hk * p.dvs[1];
+  if (p.g_split > 1) {
+    if (key < p.Nkv) {
+      const int64_t row = (((int64_t)split * p.B + b) * p.Hkv + hk) * p.Nkv + key;
+      store_partial_row<D>(dv, p.dvp + row * D, h);
+      store_partial_row<D>(dk, p.dkp + row * D, h);
+    }
+    return;
+  }
   store_grad_rows<E, D, false>(dv, dvb, p.dvs[2], key, p.Nkv, 1.f, nullptr, nullptr, 0, h);
   store_grad_rows<E, D, ROPE>(dk, dkb, p.dks[2], key, p.Nkv, p.scale, p.cos, p.sin, p.rs[0], h);
 }

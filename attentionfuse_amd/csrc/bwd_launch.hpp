@@ -11,15 +11,25 @@
 namespace af {
 
 struct BwdGrids {
-  unsigned prep, dkv, dq;
+  unsigned prep, dkv, dq, combine;   // combine: 0 unless the dK/dV head groups are split
   int waves_kv, waves_q;
 };
 
 // Workspace layout: delta (fp32, B*Hq*Nq), then with RoPE q~ (B*Hq*Nq*D) and
-// k~ (B*Hkv*Nkv*D) in the input dtype; each section 256-byte aligned.
+// k~ (B*Hkv*Nkv*D) in the input dtype, then with a head-group split the fp32
+// dK and dV partials (g_split*B*Hkv*Nkv*D each); each section 256-byte
+// aligned.
 struct BwdWorkspace {
-  size_t delta, qr, kr, total;   // byte offsets and size
+  size_t delta, qr, kr, dkp, dvp, total;   // byte offsets and size
+  int g_split;
 };
+// Workgroups of the dK/dV kernel per key block and key/value head: the
+// query heads of a group are split (a power of two dividing G) while the
+// grid stays within two workgroups per CU (512), so that a causal mask's
+// long key blocks do not leave most CUs idle.  Measured at config 5 (256
+// workgroups unsplit, one per CU): backward 1153 us unsplit, 796 us split 4
+// ways, 773 us split 2 ways; at B = 2 (512 workgroups) splitting lost.
+int bwd_group_split(const af_bwd_args& a);
 BwdWorkspace bwd_workspace_layout(const af_bwd_args& a);
 size_t bwd_workspace_bytes(const af_bwd_args& a);
 int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_t workspace_bytes,

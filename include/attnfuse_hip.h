@@ -182,7 +182,10 @@ typedef struct af_bwd_args {
 } af_bwd_args;
 
 /* Workspace bytes af_bwd needs for these arguments: delta (fp32 per query
- * row) and, with fused RoPE, the rotated q~ and k~ in the input dtype. */
+ * row); with fused RoPE the rotated q~ and k~ in the input dtype; and when
+ * the query heads of a GQA group are split over several dK/dV workgroups
+ * (grids of at most two workgroups per CU), fp32 dK and dV partial sums
+ * per split. */
 size_t af_bwd_workspace_bytes(const af_bwd_args* args);
 int af_bwd(const af_bwd_args* args, const af_blockmask* bm /* nullable */,
            void* workspace, size_t workspace_bytes, void* stream);
