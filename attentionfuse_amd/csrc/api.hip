@@ -281,8 +281,11 @@ int32_t af_decode_num_splits(int32_t batch, int32_t heads_q, int32_t heads_kv, i
   if (batch <= 0 || heads_q <= 0 || heads_kv <= 0 || seqlen_kv <= 0) return 1;
   const int g = heads_q / heads_kv;
   const int64_t groups = (int64_t)batch * heads_kv * ((g + 15) / 16);
-  // ~1024 workgroups (4 per CU on 256 CUs), at least 256 keys per split.
-  int64_t s = (1024 + groups - 1) / groups;
+  // ~512 workgroups: the split kernel keeps two steps of K/V per wave in
+  // flight in 254 VGPRs, so two 4-wave workgroups fit a CU (256 CUs); at
+  // least 256 keys per split.  Measured at config 3: 8 splits (512
+  // workgroups) 180.6 us, 16 splits 186.0 us, 12 splits 183.0 us.
+  int64_t s = (512 + groups - 1) / groups;
   s = std::min<int64_t>(s, std::max<int64_t>(1, seqlen_kv / 256));
   s = std::max<int64_t>(1, std::min<int64_t>(s, 256));
   return (int32_t)s;

@@ -92,34 +92,40 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeParams p)
   uint16_t* vt = lds + w * VT_ELEMS;
   uint32_t* vt32 = reinterpret_cast<uint32_t*>(vt);
 
-  for (int st = w; st < nsteps; st += 4) {
-    const int k0 = s_lo + 32 * st;
-    // K rows for the A operand: block kb covers keys k0 + 16 kb + c.
+  // One 32-key step of this wave: K rows (A operand of S^T, keys k0 + 16 kb
+  // + c) and V rows (lane owns keys k0 + 2c, 2c + 1 and 16-byte chunks
+  // g + 4 i) come straight from HBM into registers.
+  struct StepRegs {
     u32x4 ka[2][KSD];
+    u32x4 va[D / 32][2];
+  };
+  auto load_step = [&](int st, StepRegs& r) {
+    const int k0 = s_lo + 32 * st;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int n = k0 + 16 * kb + c;
       const bool ok = n < s_hi;
 #pragma unroll
       for (int ks = 0; ks < KSD; ++ks)
-        ka[kb][ks] = ok ? ld16(kbase + n * kstr + 32 * ks + 8 * g) : u32x4{0, 0, 0, 0};
+        r.ka[kb][ks] = ok ? ld16(kbase + n * kstr + 32 * ks + 8 * g) : u32x4{0, 0, 0, 0};
     }
-    // V rows: lane owns keys 2c, 2c+1 and 16-byte chunks g + 4 i.
-    u32x4 va[D / 32][2];
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) {
       const int dc = g + 4 * i;
       const int n = k0 + 2 * c;
-      va[i][0] = (n < s_hi) ? ld16(vbase + n * vstr + 8 * dc) : u32x4{0, 0, 0, 0};
-      va[i][1] = (n + 1 < s_hi) ? ld16(vbase + (n + 1) * vstr + 8 * dc) : u32x4{0, 0, 0, 0};
+      r.va[i][0] = (n < s_hi) ? ld16(vbase + n * vstr + 8 * dc) : u32x4{0, 0, 0, 0};
+      r.va[i][1] = (n + 1 < s_hi) ? ld16(vbase + (n + 1) * vstr + 8 * dc) : u32x4{0, 0, 0, 0};
     }
+  };
+  auto compute_step = [&](int st, const StepRegs& r) {
+    const int k0 = s_lo + 32 * st;
     // S^T blocks.
     f32x4 s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       s[kb] = f32x4{};
 #pragma unroll
-      for (int ks = 0; ks < KSD; ++ks) s[kb] = E::mfma16(ka[kb][ks], qf[ks], s[kb]);
+      for (int ks = 0; ks < KSD; ++ks) s[kb] = E::mfma16(r.ka[kb][ks], qf[ks], s[kb]);
     }
     // V^T into this wave's LDS tile: row d, column = key - k0.
 #pragma unroll
@@ -127,7 +133,7 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeParams p)
       const int dc = g + 4 * i;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const uint32_t a = va[i][0][e >> 1], bq = va[i][1][e >> 1];
+        const uint32_t a = r.va[i][0][e >> 1], bq = r.va[i][1][e >> 1];
         const uint32_t word = (e & 1) ? ((a >> 16) | (bq & 0xffff0000u))
                                       : ((a & 0xffffu) | (bq << 16));
         vt32[((8 * dc + e) * VTP + 2 * c) >> 1] = word;
@@ -139,12 +145,12 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeParams p)
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + 16 * kb + 4 * g + r;
-        float v = s[kb][r] * c2;
+      for (int rr = 0; rr < 4; ++rr) {
+        const int key = k0 + 16 * kb + 4 * g + rr;
+        float v = s[kb][rr] * c2;
         if constexpr (BIAS == 1) v -= slope2 * (float)abs((p.Nkv - 1) - key);
         v = key < s_hi ? v : -INFINITY;
-        x[4 * kb + r] = v;
+        x[4 * kb + rr] = v;
         mx = fmaxf(mx, v);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -179,6 +185,17 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeParams p)
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  // The loads of step st + 4 are issued before step st is computed, so each
+  // wave keeps two steps (16 KB at D = 128) of K/V in flight.
+  StepRegs ra, rb;
+  if (w < nsteps) load_step(w, ra);
+  for (int st = w; st < nsteps; st += 8) {
+    if (st + 4 < nsteps) load_step(st + 4, rb);
+    compute_step(st, ra);
+    if (st + 4 >= nsteps) break;
+    if (st + 8 < nsteps) load_step(st + 8, ra);
+    compute_step(st + 4, rb);
   }
 
   // ---- merge the four waves through LDS ------------------------------------
