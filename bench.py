@@ -159,6 +159,41 @@ def bench_decode(steps, warmup):
     return _time_launch(launch, steps, warmup)
 
 
+def bench_decode_latency(steps, warmup):
+    """Per-call latency of a short-cache decode step (B=1, Llama-3-8B heads,
+    cache 1024, bf16), where launch and host costs dominate: prepared
+    launches (one ctypes call per step) and the same call replayed from a
+    captured HIP graph of 16 steps."""
+    import torch
+
+    import attnfuse as af
+    from attentionfuse_amd.runtime.prepared import prepare_decode
+
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, N, D = 1, 32, 8, 1024, 128
+    g = torch.Generator(device=dev).manual_seed(0)
+    Q = torch.randn(B, Hq, 1, D, generator=g, device=dev, dtype=torch.bfloat16)
+    K = torch.randn(B, Hkv, N, D, generator=g, device=dev, dtype=torch.bfloat16)
+    V = torch.randn(B, Hkv, N, D, generator=g, device=dev, dtype=torch.bfloat16)
+    dense = af.attention(lambda Q, K, V: af.softmax(af.scaled_dot_product(Q, K)) @ V)
+    launch, _ = prepare_decode(dense(Q, K, V, return_graph=True), Q, K, V)
+    eager_ms = _time_launch(launch, steps, warmup)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    reps = 16
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            launch()
+    graph_ms = _time_launch(graph.replay, max(steps // reps, 2), 1) / reps
+    return {"workload": "decode B=1 Hq=32 Hkv=8 D=128 bf16, cache 1024",
+            "eager_us": round(eager_ms * 1e3, 2), "graph_us": round(graph_ms * 1e3, 2)}
+
+
 def bench_bigbird(steps, warmup):
     """Config 4: block-sparse forward (saving the LSE) + backward."""
     import torch
@@ -391,6 +426,7 @@ def main():
                           "bound": "hbm", "peak": PEAK_HBM_GBS,
                           "frac": round(gbs / PEAK_HBM_GBS, 4),
                           "algorithmic_bytes_per_launch": nbytes}
+        line["decode_latency"] = bench_decode_latency(args.steps, args.warmup)
     if not args.no_train:
         line["bigbird"] = bench_bigbird(max(args.steps // 2, 1), max(args.warmup // 2, 1))
         line["train"] = bench_train(max(args.steps // 2, 1), max(args.warmup // 2, 1))
