@@ -169,6 +169,13 @@ __device__ __forceinline__ void buf_ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds
                                            16, byte_off, 0, 0, 0);
 }
 
+// 4 bytes per lane from the buffer straight into LDS: lane l's bytes land at
+// lds_base + 4 l.
+__device__ __forceinline__ void buf_ld4_lds(__amdgpu_buffer_rsrc_t r, void* lds_base, uint32_t byte_off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base,
+                                           4, byte_off, 0, 0, 0);
+}
+
 // ---------------------------------------------------------------------------
 // Transposed LDS read (ds_read_b64_tr_b16).  Within each 16-lane group,
 // result lane L, element i is element (L % 4) of the 64-bit chunk addressed
@@ -179,7 +186,12 @@ __device__ __forceinline__ void buf_ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds
 // ---------------------------------------------------------------------------
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+// The pointer is __restrict__ so the read carries alias-scope metadata: the
+// compiler then does not hold it behind an s_waitcnt vmcnt(0) for every load
+// into LDS still in flight (the kernels order those with explicit waits and
+// barriers; without the qualifier each transposing read waited for the
+// prefetch of the next tile).
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* __restrict__ p) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) s16x4*)(p));
   return __builtin_bit_cast(u32x2, v);

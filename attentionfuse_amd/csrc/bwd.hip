@@ -26,8 +26,8 @@ BwdWorkspace bwd_workspace_layout(const af_bwd_args& a) {
     return w;
   const size_t rows_q = (size_t)a.batch * a.heads_q * a.seqlen_q;
   const size_t rows_k = (size_t)a.batch * a.heads_kv * a.seqlen_kv;
-  w.delta = 0;
-  w.total = up(rows_q * sizeof(float));
+  w.ld = 0;
+  w.total = up(rows_q * 2 * sizeof(float));
   if (a.key.rope) {
     w.qr = w.total;
     w.total += up(rows_q * a.key.head_dim * 2);
@@ -112,7 +112,7 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   p.dout = static_cast<const uint16_t*>(a->dout);
   p.lse = a->lse;
   char* ws = static_cast<char*>(workspace);
-  p.delta = reinterpret_cast<float*>(ws + wl.delta);
+  p.ld = reinterpret_cast<float*>(ws + wl.ld);
   if (k.rope) {
     p.qr = reinterpret_cast<uint16_t*>(ws + wl.qr);
     p.kr = reinterpret_cast<uint16_t*>(ws + wl.kr);

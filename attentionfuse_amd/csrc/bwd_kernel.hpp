@@ -15,7 +15,8 @@
 // attnfuse/runtime/backward.py:77-79).
 //
 // Decomposition:
-//  * bwd_prep_kernel: delta per query row, and with RoPE the rotated q~ and
+//  * bwd_prep_kernel: delta and L log2(e) per query row (one 8-byte pair,
+//    streamed into LDS with the query tiles), and with RoPE the rotated q~ and
 //    k~ written once to the workspace, rounded to the input dtype exactly as
 //    the forward rounds them in registers.  Every query tile is read by all
 //    key blocks (and every key tile by all query blocks), so rotating once
@@ -53,7 +54,10 @@ struct BwdParams {
   const uint16_t* o;
   const uint16_t* dout;
   const float* lse;
-  float* delta;            // (B, Hq, Nq) fp32 workspace
+  // (B, Hq, Nq) fp32 pairs {L log2(e) (0 for a row that sees no key),
+  // delta}, workspace: one row's pair is 8 contiguous bytes, so a query
+  // tile's 32 pairs load into LDS with one wave instruction
+  float* ld;
   uint16_t* qr;            // RoPE: q~ workspace, (B, Hq, Nq, D) contiguous
   uint16_t* kr;            // RoPE: k~ workspace, (B, Hkv, Nkv, D) contiguous
   const uint16_t* qt;      // q~ as the score kernels read it (qr, or q)
@@ -88,7 +92,8 @@ struct BwdParams {
 };
 
 // ---------------------------------------------------------------------------
-// delta = rowsum(dO * O), fp32; with RoPE also q~ and k~ into the workspace.
+// delta = rowsum(dO * O) and L log2(e), fp32; with RoPE also q~ and k~ into
+// the workspace.
 // A row is handled by D/16 threads, thread j holding the rotate-half pair of
 // chunks j and j + D/16.  Rows [0, B*Hq*Nq) are query rows, the next
 // B*Hkv*Nkv (RoPE only) key rows.
@@ -118,7 +123,10 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(const BwdParams p) {
     }
 #pragma unroll
     for (int off = 1; off < TPR; off <<= 1) acc += __shfl_xor(acc, off, 64);
-    if (j == 0) p.delta[r] = acc;
+    if (j == 0) {
+      const float L = p.lse[b * p.ls[0] + hq * p.ls[1] + i * p.ls[2]];
+      *reinterpret_cast<f32x2*>(p.ld + 2 * r) = f32x2{(L == -INFINITY) ? 0.f : L * kLog2e, acc};
+    }
     if constexpr (ROPE) {
       rope_row_chunk<E, D>(p.q + b * p.qs[0] + hq * p.qs[1] + i * p.qs[2], p.cos + i * p.rs[0],
                            p.sin + i * p.rs[0], p.qr + r * D, j);
@@ -293,7 +301,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   constexpr int KS = D / 16, DB = D / 32;
   constexpr bool VLDS = D > 64;            // V block in LDS instead of registers
   constexpr int TILE = 32 * D;             // one 32-row tile (elements)
-  constexpr int STAGE = 2 * TILE + 128;    // q~ tile, dO tile, 32 L + 32 delta floats
+  constexpr int STAGE = 2 * TILE + 128;    // q~ tile, dO tile, 32 (L log2 e, delta) pairs
   constexpr int VBLK = VLDS ? BK * D : 0;
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE + VBLK];
 
@@ -370,28 +378,19 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
 
   TileDma<D, NT> dma;
   dma.init(w, lane, p.qts[2], p.dos[2]);
-  float lreg = 0.f, dreg = 0.f;
-  // issue the tile loads of stage t into LDS slot `slot`, and fetch its L / delta
+  // issue the loads of stage t into LDS slot `slot`: the q~ and dO tiles,
+  // and (wave 0) the tile's 32 (L log2 e, delta) pairs; rows past N_q load
+  // as zeros
   auto stage_load = [&](int t, int slot) {
     const int gi = t / ntq, hq = hq0 + gi;
     const int m0 = tile_m0(t - gi * ntq);
     dma.load(lds, slot * STAGE, w, p.qt + b * p.qts[0] + hq * p.qts[1], p.qts[2], p.Nq,
              p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], p.Nq, m0);
-    if (tid < 64) {
-      const int row = m0 + (tid & 31);
-      const bool ok = row < p.Nq;
-      if (tid < 32) {
-        const float L = ok ? p.lse[b * p.ls[0] + hq * p.ls[1] + row * p.ls[2]] : 0.f;
-        lreg = (L == -INFINITY) ? 0.f : L * kLog2e;
-      } else {
-        dreg = ok ? p.delta[((int64_t)b * p.Hq + hq) * p.Nq + row] : 0.f;
-      }
+    if (w == 0) {
+      const int64_t row0 = ((int64_t)b * p.Hq + hq) * p.Nq + m0;
+      const auto rs = make_rsrc(p.ld + 2 * row0, (uint32_t)max(p.Nq - m0, 0) * 8u);
+      buf_ld4_lds(rs, lds + slot * STAGE + 2 * TILE, (uint32_t)lane * 4u);
     }
-  };
-  auto stage_store = [&](int slot) {
-    float* f = reinterpret_cast<float*>(lds + slot * STAGE + 2 * TILE);
-    if (tid < 32) f[tid] = lreg;
-    else if (tid < 64) f[tid] = dreg;
   };
 
   f32x16 dk[DB], dv[DB];
@@ -404,10 +403,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   constexpr bool kAlibiOneSided = BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW);
   const int qr_row = kperm(c);   // tile row of this lane's (permuted) query
 
-  if (ntiles > 0) {
-    stage_load(0, 0);
-    stage_store(0);
-  }
+  if (ntiles > 0) stage_load(0, 0);
   wait_lds_dma();
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
@@ -418,8 +414,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
     const uint16_t* buf = lds + (t & 1) * STAGE;
     const uint16_t* Qs = buf;
     const uint16_t* Os = buf + TILE;
-    const float* Ls = reinterpret_cast<const float*>(buf + 2 * TILE);
-    const float* Dl = Ls + 32;
+    const float* LD = reinterpret_cast<const float*>(buf + 2 * TILE);
 
     bool active = n0w < p.Nkv && m0 < p.Nq;
     if constexpr (MASK == MASK_CAUSAL) active = active && m0 + 31 >= n0w;
@@ -476,16 +471,16 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
       u32x4 pp[2], pd[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const f32x4 l4a = *reinterpret_cast<const f32x4*>(Ls + 16 * j + 8 * h);
-        const f32x4 l4b = *reinterpret_cast<const f32x4*>(Ls + 16 * j + 8 * h + 4);
-        const f32x4 d4a = *reinterpret_cast<const f32x4*>(Dl + 16 * j + 8 * h);
-        const f32x4 d4b = *reinterpret_cast<const f32x4*>(Dl + 16 * j + 8 * h + 4);
+        // pairs of tile rows 16 j + 8 h .. + 7
+        f32x4 ld4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ld4[i] = *reinterpret_cast<const f32x4*>(LD + 2 * (16 * j + 8 * h) + 4 * i);
         float pv[8], dsv[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int r = 8 * j + e;
-          const float L2 = e < 4 ? l4a[e] : l4b[e - 4];
-          const float dl = e < 4 ? d4a[e] : d4b[e - 4];
+          const float L2 = ld4[e >> 1][2 * (e & 1)];
+          const float dl = ld4[e >> 1][2 * (e & 1) + 1];
           const float pr = __builtin_amdgcn_exp2f(s[r] - L2);
           pv[e] = pr;
           dsv[e] = pr * (dp[r] - dl);
@@ -512,7 +507,6 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
         }
       }
     }
-    if (more) stage_store((t + 1) & 1);
     wait_lds_dma();
     __syncthreads();
   }
@@ -562,9 +556,9 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   load_operand_rows<D>(of, p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], qrow, p.Nq, h);
   float L2 = 0.f, dl = 0.f;
   if (qrow < p.Nq) {
-    const float L = p.lse[b * p.ls[0] + hq * p.ls[1] + qrow * p.ls[2]];
-    L2 = (L == -INFINITY) ? 0.f : L * kLog2e;
-    dl = p.delta[((int64_t)b * p.Hq + hq) * p.Nq + qrow];
+    const f32x2 ld = *reinterpret_cast<const f32x2*>(p.ld + 2 * (((int64_t)b * p.Hq + hq) * p.Nq + qrow));
+    L2 = ld[0];
+    dl = ld[1];
   }
 
   int n_lo = 0, n_hi = p.Nkv, ntiles;

@@ -15,12 +15,12 @@ struct BwdGrids {
   int waves_kv, waves_q;
 };
 
-// Workspace layout: delta (fp32, B*Hq*Nq), then with RoPE q~ (B*Hq*Nq*D) and
-// k~ (B*Hkv*Nkv*D) in the input dtype, then with a head-group split the fp32
-// dK and dV partials (g_split*B*Hkv*Nkv*D each); each section 256-byte
-// aligned.
+// Workspace layout: (L log2 e, delta) fp32 pairs (B*Hq*Nq), then with RoPE
+// q~ (B*Hq*Nq*D) and k~ (B*Hkv*Nkv*D) in the input dtype, then with a
+// head-group split the fp32 dK and dV partials (g_split*B*Hkv*Nkv*D each);
+// each section 256-byte aligned.
 struct BwdWorkspace {
-  size_t delta, qr, kr, dkp, dvp, total;   // byte offsets and size
+  size_t ld, qr, kr, dkp, dvp, total;   // byte offsets and size
   int g_split;
 };
 // Workgroups of the dK/dV kernel per key block and key/value head: the

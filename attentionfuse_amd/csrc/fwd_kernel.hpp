@@ -11,17 +11,18 @@
 // Work decomposition (MI355X-first, not a translation):
 //  * a workgroup owns BM = 32*WAVES query rows of one (batch, head); each
 //    wave64 owns 32 rows: one 32x32 MFMA output block.
-//  * K and V stream through LDS in 64-key stages, double-buffered: buffer
-//    loads for stage t+1 are in flight while stage t is on the MFMA pipes.
-//    The loads go through raw buffer resources, so rows past N_kv come back
-//    as zeros from the hardware bounds check (no clamps, no branches).
-//    K is rotated (RoPE) once per stage while it is written to LDS; V is
-//    written row-major and read back transposed by ds_read_b64_tr_b16.
+//  * K and V stream through LDS in 64-key stages, two slots each, loaded
+//    global -> LDS by buffer_load ... lds while earlier stages are on the
+//    MFMA pipes.  The loads go through raw buffer resources, so rows past
+//    N_kv come back as zeros from the hardware bounds check (no clamps, no
+//    branches).  With RoPE, K arrives already rotated (rope_rows_kernel
+//    writes k~ once per call); V is written row-major and read back
+//    transposed by ds_read_b64_tr_b16.
 //  * scores are computed transposed (S^T = K Q^T): each lane then holds 32
 //    keys of one query, so the row max is in-register plus one
 //    v_permlane32_swap, and P^T is the B operand of the P*V MFMA without any
-//    register shuffle (see af_common.hpp).  Row sums come from the MFMA pipe
-//    (an all-ones A operand times P^T).
+//    register shuffle (see af_common.hpp).  Row sums add the rounded P on
+//    the VALU in fp32.
 //  * the softmax max is lazy: the running max only moves when a score
 //    exceeds it by more than 2^kTau, so the O rescale is rare.
 //  * Q stays in registers for the whole kernel, rotated once.

@@ -181,8 +181,8 @@ typedef struct af_bwd_args {
   int32_t window;
 } af_bwd_args;
 
-/* Workspace bytes af_bwd needs for these arguments: delta (fp32 per query
- * row); with fused RoPE the rotated q~ and k~ in the input dtype; and when
+/* Workspace bytes af_bwd needs for these arguments: the log2-scaled LSE and
+ * delta (an fp32 pair per query row); with fused RoPE the rotated q~ and k~ in the input dtype; and when
  * the query heads of a GQA group are split over several dK/dV workgroups
  * (grids of at most two workgroups per CU), fp32 dK and dV partial sums
  * per split. */
