@@ -55,6 +55,20 @@ struct F16 {
     asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]" : "+v"(lo) : "v"(w));
     asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(hi) : "v"(w));
   }
+  // lo = w.lo, hi = w.hi in fp32 (starts two sums without zeroing them)
+  __device__ static inline void first_pair(uint32_t w, float& lo, float& hi) {
+    asm("v_fma_mix_f32 %0, %1, 1.0, 0 op_sel_hi:[1,0,0]" : "=v"(lo) : "v"(w));
+    asm("v_fma_mix_f32 %0, %1, 1.0, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(hi) : "v"(w));
+  }
+  // Call after the last add_pair into four sums, before ordinary code reads
+  // them.  The compiler's hazard recognizer keeps dependent asm statements
+  // two wait states apart, but it does not look at a compiler-generated
+  // reader of an asm result, which then could issue right behind the last
+  // v_fma_mix_f32.  Tying the sums through the nop gives that reader the
+  // same separation (a precaution; it costs two cycles per tile).
+  __device__ static inline void sums_ready(float& a, float& b, float& c, float& d) {
+    asm volatile("s_nop 1" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+  }
 };
 
 struct BF16 {
@@ -88,6 +102,13 @@ struct BF16 {
     lo += __builtin_bit_cast(float, w << 16);
     hi += __builtin_bit_cast(float, w & 0xffff0000u);
   }
+  // lo = w.lo, hi = w.hi in fp32
+  __device__ static inline void first_pair(uint32_t w, float& lo, float& hi) {
+    lo = __builtin_bit_cast(float, w << 16);
+    hi = __builtin_bit_cast(float, w & 0xffff0000u);
+  }
+  // the sums are ordinary compiler-generated code
+  __device__ static inline void sums_ready(float&, float&, float&, float&) {}
 };
 
 // Unpack a 16-byte chunk into 8 floats / pack 8 floats into a chunk.

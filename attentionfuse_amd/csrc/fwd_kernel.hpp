@@ -180,8 +180,10 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   RowsDma<D, NT, BN> kdma, vdma;
   kdma.init(w, lane, kstr);
   vdma.init(w, lane, vstr);
-  auto load_k = [&](int t) { kdma.load(lds, (t & 1) * TILE, w, kbase, kstr, p.Nkv, tile_n0(t)); };
-  auto load_v = [&](int t) { vdma.load(lds, (2 + (t & 1)) * TILE, w, vbase, vstr, p.Nkv, tile_n0(t)); };
+  // slot parity t & 1 is passed as a literal by the unrolled pipeline so
+  // that every LDS address is a register plus an immediate offset
+  auto load_k = [&](int t, int par) { kdma.load(lds, par * TILE, w, kbase, kstr, p.Nkv, tile_n0(t)); };
+  auto load_v = [&](int t, int par) { vdma.load(lds, (2 + par) * TILE, w, vbase, vstr, p.Nkv, tile_n0(t)); };
   // per-lane LDS offsets: the K rows of the S^T MFMA (key block 0; block 1 is
   // 32 rows on, same swizzle) and the transposed V reads of the P V MFMA
   int koff[KS];
@@ -233,8 +235,8 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   if constexpr (BIAS == BIAS_ADD) brow = p.bias + b * p.bs[0] + hq * p.bs[1] + (int64_t)qrow * p.bs[2];
 
   // S^T = K Q^T of tile t (two 32-key blocks), K from its LDS slot.
-  auto scores = [&](int t, f32x16* s) {
-    const uint16_t* Ks = lds + (t & 1) * TILE;
+  auto scores = [&](int par, f32x16* s) {
+    const uint16_t* Ks = lds + par * TILE;
 #pragma unroll
     for (int kb = 0; kb < BN / 32; ++kb) {
       s[kb] = sinit;
@@ -243,13 +245,30 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     }
   };
 
-  // Bias, mask and running max of tile t's scores s (with the rare O
-  // rescale); returns the affine map (zc, off) from a score to its logit
-  // minus the running max.
+  // S^T of tile t recomputed from K in global memory, for the rare step that
+  // must move the running max after its K slot has been refilled.  Same
+  // operand layout as the LDS reads above; keys past N_kv read as zeros
+  // (their scores are masked).
+  auto scores_global = [&](int t, f32x16* s) {
+    const int n0 = tile_n0(t);
+    const auto kr = make_rsrc(kbase + (int64_t)n0 * kstr, span_bytes<D>(p.Nkv - n0, kstr));
+#pragma unroll
+    for (int kb = 0; kb < BN / 32; ++kb) {
+      const uint32_t row = (uint32_t)((32 * kb + kperm(c)) * kstr + 8 * h) * 2u;
+      s[kb] = sinit;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) s[kb] = E::mfma32(buf_ld16(kr, row + 32u * ks), qf[ks], s[kb]);
+    }
+  };
+
+  // Affine map (zc, off[kb]) from a score of key block kb to its logit minus
+  // the running max (log2 units for softmax, natural units for relu).
   struct Logit {
     float zc, off[BN / 32];
   };
-  auto prepare = [&](int t, f32x16* s) -> Logit {
+  // Bias and mask of tile t's scores s; returns the map without the running
+  // max.  `count` adds the tile to the coverage counters (once per tile).
+  auto bias_mask = [&](int t, f32x16* s, bool count) -> Logit {
     const int n0 = tile_n0(t);
     bool active = q0w < p.Nq && n0 >= 0 && n0 < p.Nkv;
     if constexpr (MASK == MASK_CAUSAL) active = active && n0 <= q0w + 31;
@@ -261,138 +280,137 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     // A wave whose rows see nothing of this stage still runs it (all its
     // scores are masked, so P = 0 and O, l are unchanged): a branch around
     // the MFMAs would force the accumulators through copies every iteration.
-    if (active && p.coverage != nullptr && lane == 0) {
+    if (count && active && p.coverage != nullptr && lane == 0) {
       const int64_t ci = ((int64_t)(b * p.Hq + hq) * p.cov_nq + (q0w >> 5)) * p.cov_nk + (n0 >> 6);
       atomicAdd(p.coverage + ci, 1u);
     }
-    {
-      bool need_mask = !active || n0 + BN > p.Nkv;
-      if constexpr (MASK == MASK_CAUSAL) need_mask = need_mask || n0 + BN - 1 > q0w;
-      if constexpr (MASK == MASK_SW)
-        need_mask = need_mask || (q0w + 31 - n0 >= p.window) || (n0 + BN - 1 - q0w >= p.window);
-      if constexpr (MASK == MASK_CSW)
-        need_mask = need_mask || (q0w + 31 - n0 >= p.window) || n0 + BN - 1 > q0w;
+    bool need_mask = !active || n0 + BN > p.Nkv;
+    if constexpr (MASK == MASK_CAUSAL) need_mask = need_mask || n0 + BN - 1 > q0w;
+    if constexpr (MASK == MASK_SW)
+      need_mask = need_mask || (q0w + 31 - n0 >= p.window) || (n0 + BN - 1 - q0w >= p.window);
+    if constexpr (MASK == MASK_CSW)
+      need_mask = need_mask || (q0w + 31 - n0 >= p.window) || n0 + BN - 1 > q0w;
 
-      // Logit of element r of key block kb: s[r] * zc + zoff[kb] (log2 units
-      // for softmax, natural units for relu).
-      float zc = zc0;
-      float zoff[BN / 32];
+    Logit lg;
+    lg.zc = zc0;
+#pragma unroll
+    for (int kb = 0; kb < BN / 32; ++kb)
+      lg.off[kb] = kAlibiOneSided ? aslope * (float)(n0 + 32 * kb + 8 * h - qrow) : 0.f;
+    if constexpr (BIAS == BIAS_ADD) {
+      const float bscale = (NORM == NORM_SOFTMAX) ? kLog2e : 1.f;
 #pragma unroll
       for (int kb = 0; kb < BN / 32; ++kb)
-        zoff[kb] = kAlibiOneSided ? aslope * (float)(n0 + 32 * kb + 8 * h - qrow) : 0.f;
-      if constexpr (BIAS == BIAS_ADD) {
-        const float bscale = (NORM == NORM_SOFTMAX) ? kLog2e : 1.f;
 #pragma unroll
-        for (int kb = 0; kb < BN / 32; ++kb)
+        for (int j = 0; j < 2; ++j) {
+          const int key0 = n0 + 32 * kb + 16 * j + 8 * h;
+          float bv[8];
+          if (qrow < p.Nq && key0 + 8 <= p.Nkv) {
+            unpack8<E>(ld16(brow + key0 * p.bs[3]), bv);
+          } else {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int key0 = n0 + 32 * kb + 16 * j + 8 * h;
-            float bv[8];
-            if (qrow < p.Nq && key0 + 8 <= p.Nkv) {
-              unpack8<E>(ld16(brow + key0 * p.bs[3]), bv);
-            } else {
-#pragma unroll
-              for (int e = 0; e < 8; ++e) {
-                const uint16_t raw = (qrow < p.Nq && key0 + e < p.Nkv) ? brow[(key0 + e) * p.bs[3]] : 0;
-                bv[e] = E::lo(raw);
-              }
+            for (int e = 0; e < 8; ++e) {
+              const uint16_t raw = (qrow < p.Nq && key0 + e < p.Nkv) ? brow[(key0 + e) * p.bs[3]] : 0;
+              bv[e] = E::lo(raw);
             }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) s[kb][8 * j + e] = __builtin_fmaf(s[kb][8 * j + e], zc, bv[e] * bscale);
           }
-        zc = 1.f;
-      } else if constexpr (BIAS == BIAS_ALIBI) {
-        if constexpr (!kAlibiOneSided) {
-          // two-sided windows: -slope |i - j| per element
 #pragma unroll
-          for (int kb = 0; kb < BN / 32; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int key = n0 + 32 * kb + acc_key(r, h);
-              s[kb][r] = __builtin_fmaf(s[kb][r], zc, -aslope * (float)abs(qrow - key));
-            }
-          zc = 1.f;
+          for (int e = 0; e < 8; ++e) s[kb][8 * j + e] = __builtin_fmaf(s[kb][8 * j + e], lg.zc, bv[e] * bscale);
         }
-      }
-      if (need_mask) {
+      lg.zc = 1.f;
+    } else if constexpr (BIAS == BIAS_ALIBI) {
+      if constexpr (!kAlibiOneSided) {
+        // two-sided windows: -slope |i - j| per element
 #pragma unroll
         for (int kb = 0; kb < BN / 32; ++kb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = n0 + 32 * kb + acc_key(r, h);
-            bool ok = key < p.Nkv;
-            if constexpr (MASK == MASK_CAUSAL) ok = ok && key <= qrow;
-            if constexpr (MASK == MASK_SW) ok = ok && abs(qrow - key) < p.window;
-            if constexpr (MASK == MASK_CSW) ok = ok && key <= qrow && qrow - key < p.window;
-            s[kb][r] = ok ? s[kb][r] : -INFINITY;
+            s[kb][r] = __builtin_fmaf(s[kb][r], lg.zc, -aslope * (float)abs(qrow - key));
           }
-      }
-
-      if constexpr (NORM == NORM_SOFTMAX) {
-        float mz = -INFINITY;
-        if constexpr (kAlibiOneSided) {
-#pragma unroll
-          for (int kb = 0; kb < BN / 32; ++kb) {
-            float mk = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mk = fmaxf(mk, s[kb][r]);
-            mz = fmaxf(mz, __builtin_fmaf(mk, zc, zoff[kb]));
-          }
-        } else {
-#pragma unroll
-          for (int kb = 0; kb < BN / 32; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mz = fmaxf(mz, s[kb][r]);
-          mz = __builtin_fmaf(mz, zc, zoff[0]);
-        }
-        const float mx = max_xor32(mz);
-        // The rescale runs only when some row of the wave grew past the
-        // slack.  It multiplies the accumulators in place (tied asm
-        // operands): written as plain C++ inside the branch, the register
-        // allocator gives the two paths different registers and copies every
-        // accumulator on every iteration.  The s_nops give the MFMA->VALU
-        // and VALU->MFMA dependencies on the accumulators their wait states,
-        // which the hazard recognizer cannot see through the asm; alpha is an
-        // operand of the nops so its v_exp is issued before them.
-        const bool grow = mx > m_run + kTau;
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-          const float m_new = grow ? mx : m_run;
-          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-          asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : : "v"(alpha));
-#pragma unroll
-          for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              float x = o[db][r];
-              asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x) : "v"(alpha));
-              o[db][r] = x;
-            }
-          lsum[0] *= alpha;
-          lsum[1] *= alpha;
-          asm volatile("s_nop 7");
-          m_run = m_new;
-        }
-        Logit lg;
-        lg.zc = zc;
-#pragma unroll
-        for (int kb = 0; kb < BN / 32; ++kb) lg.off[kb] = zoff[kb] - m_run;
-        return lg;
-      } else {
-        Logit lg;
-        lg.zc = zc;
-#pragma unroll
-        for (int kb = 0; kb < BN / 32; ++kb) lg.off[kb] = zoff[kb];
-        return lg;
+        lg.zc = 1.f;
       }
     }
+    if (need_mask) {
+      // Register r of key block kb holds key base + kr(r), base = n0 + 32 kb
+      // + 8h, kr(r) = 16 (r/8) + r%8: every condition is a range lo <= kr <=
+      // hi, one or two compares against a constant per element.
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb) {
+        const int base = n0 + 32 * kb + 8 * h;
+        int hi = p.Nkv - 1 - base;
+        int lo = 0;
+        if constexpr (MASK == MASK_CAUSAL || MASK == MASK_CSW) hi = min(hi, qrow - base);
+        if constexpr (MASK == MASK_SW) hi = min(hi, qrow + p.window - 1 - base);
+        if constexpr (MASK == MASK_SW || MASK == MASK_CSW) lo = qrow - p.window + 1 - base;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kr = 16 * (r >> 3) + (r & 7);
+          bool ok = kr <= hi;
+          if constexpr (MASK == MASK_SW || MASK == MASK_CSW) ok = ok && kr >= lo;
+          s[kb][r] = ok ? s[kb][r] : -INFINITY;
+        }
+      }
+    }
+    return lg;
   };
 
-  // The straight-line body of one pipeline step, one basic block: the score
-  // MFMAs of tile t+1 into nxt, P = 2^(logit) (or relu) of tile t with its
-  // row sums, and O += P V(t).
-  auto exp_pv = [&](int t, f32x16* s, f32x16* nxt, Logit lg) {
-    scores(t + 1, nxt);
-    const uint16_t* Vs = lds + (2 + (t & 1)) * TILE;
+  // Running max of the biased, masked scores s of one tile (softmax only):
+  // moves m_run when some row grew past the slack, with the O / l rescale,
+  // and returns lg with the running max subtracted.
+  auto rebase = [&](const f32x16* s, Logit lg) -> Logit {
+    if constexpr (NORM == NORM_SOFTMAX) {
+      float mz = -INFINITY;
+      if constexpr (kAlibiOneSided) {
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb) {
+          float mk = -INFINITY;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mk = fmaxf(mk, s[kb][r]);
+          mz = fmaxf(mz, __builtin_fmaf(mk, lg.zc, lg.off[kb]));
+        }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mz = fmaxf(mz, s[kb][r]);
+        mz = __builtin_fmaf(mz, lg.zc, lg.off[0]);
+      }
+      const float mx = max_xor32(mz);
+      // The rescale runs only when some row of the wave grew past the
+      // slack.  It multiplies the accumulators in place (tied asm
+      // operands): written as plain C++ inside the branch, the register
+      // allocator gives the two paths different registers and copies every
+      // accumulator on every iteration.  The s_nops give the MFMA->VALU
+      // and VALU->MFMA dependencies on the accumulators their wait states,
+      // which the hazard recognizer cannot see through the asm; alpha is an
+      // operand of the nops so its v_exp is issued before them.
+      const bool grow = mx > m_run + kTau;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float m_new = grow ? mx : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : : "v"(alpha));
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float x = o[db][r];
+            asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x) : "v"(alpha));
+            o[db][r] = x;
+          }
+        lsum[0] *= alpha;
+        lsum[1] *= alpha;
+        asm volatile("s_nop 7");
+        m_run = m_new;
+      }
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb) lg.off[kb] -= m_run;
+    }
+    return lg;
+  };
+
+  // P = 2^(logit) (or relu) of one tile in place and its rounded 16-bit P^T
+  // as the B operands of the P V MFMA (one per 16 keys).
+  auto softmax_tile = [&](f32x16* s, const Logit& lg, u32x4* pf) {
 #pragma unroll
     for (int kb = 0; kb < BN / 32; ++kb)
 #pragma unroll
@@ -400,20 +418,37 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
         const float x = __builtin_fmaf(s[kb][r], lg.zc, lg.off[kb]);
         s[kb][r] = (NORM == NORM_SOFTMAX) ? __builtin_amdgcn_exp2f(x) : fmaxf(x, 0.f);
       }
-    // P^T (registers) -> B operands, one per 16 keys.
-    u32x4 pf[BN / 16];
 #pragma unroll
     for (int kk = 0; kk < BN / 16; ++kk) {
       const int kb = kk >> 1, j = kk & 1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) pf[kk][i] = E::pack(s[kb][8 * j + 2 * i], s[kb][8 * j + 2 * i + 1]);
     }
-    // row sums of the rounded P (this lane's 32 keys; the partner lane
-    // l ^ 32 holds the other 32), fp32, two chains
+  };
+  // fp32 sums of the rounded P over this lane's 32 keys (the partner lane
+  // l ^ 32 holds the other 32): added into the two running chains ...
+  auto add_rowsum = [&](const u32x4* pf) {
 #pragma unroll
     for (int kk = 0; kk < BN / 16; ++kk)
 #pragma unroll
       for (int i = 0; i < 4; ++i) E::add_pair(pf[kk][i], lsum[0], lsum[1]);
+  };
+  // ... or summed alone, over four chains, for the test of a lazy step
+  auto tile_rowsum = [&](const u32x4* pf) -> float {
+    float ts[4];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) E::first_pair(pf[kk][0], ts[2 * kk], ts[2 * kk + 1]);
+#pragma unroll
+    for (int kk = 0; kk < BN / 16; ++kk)
+#pragma unroll
+      for (int i = kk < 2 ? 1 : 0; i < 4; ++i) E::add_pair(pf[kk][i], ts[2 * (kk & 1)], ts[2 * (kk & 1) + 1]);
+    E::sums_ready(ts[0], ts[1], ts[2], ts[3]);
+    return (ts[0] + ts[1]) + (ts[2] + ts[3]);
+  };
+
+  // O += P V(t), V^T read transposed from its LDS slot.
+  auto pv = [&](int par, const u32x4* pf) {
+    const uint16_t* Vs = lds + (2 + par) * TILE;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
@@ -427,37 +462,114 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     }
   };
 
+  // One step with the running max computed first (every step for relu and
+  // ALiBi; the first step otherwise): bias, mask and max of tile t, then the score
+  // MFMAs of tile t+1 in the same basic block as P of tile t, and P V(t).
+  auto step_exact = [&](int t, int par, f32x16* s, f32x16* nxt) {
+    const Logit lg = rebase(s, bias_mask(t, s, true));
+    scores(par ^ 1, nxt);
+    u32x4 pf[BN / 16];
+    softmax_tile(s, lg, pf);
+    add_rowsum(pf);
+    pv(par, pf);
+  };
+
+  // Later softmax steps skip the max: P is taken against the current
+  // running max, and the sums of the rounded P then tell whether the max has
+  // to move.  If every lane's sum is below 2^kRedo, every P of the tile is
+  // below 2^kRedo -- finite in fp16 and bf16, like the P <= 2^kTau of the
+  // exact step -- and the step stands.  Otherwise (a row grew by more than
+  // kRedo, or meets its first visible keys: m_run = -1e30 makes every P
+  // infinite) the scores of tile t are recomputed from global memory, its K
+  // slot already holding tile t+2, and the step runs exactly.  This saves
+  // the max (16 v_max3, a lane swap and the compare) on almost every tile.
+  constexpr float kRedo = 8192.f;  // 2^13
+  auto step_lazy = [&](int t, int par, f32x16* s, f32x16* nxt) {
+    const Logit lg0 = bias_mask(t, s, true);
+    Logit lg = lg0;
+#pragma unroll
+    for (int kb = 0; kb < BN / 32; ++kb) lg.off[kb] -= m_run;
+    scores(par ^ 1, nxt);
+    u32x4 pf[BN / 16];
+    softmax_tile(s, lg, pf);
+    float tsum = tile_rowsum(pf);
+    if (__builtin_amdgcn_ballot_w64(!(tsum < kRedo)) != 0) {
+      scores_global(t, s);
+      const Logit lg1 = rebase(s, bias_mask(t, s, false));
+      softmax_tile(s, lg1, pf);
+      tsum = tile_rowsum(pf);
+    }
+    lsum[0] += tsum;
+    pv(par, pf);
+  };
+
   // ---- software pipeline ---------------------------------------------------
-  // Iteration t issues the loads of K(t+2) and V(t+1), masks tile t and
-  // updates the running max, then runs the score MFMAs of tile t+1 (on the
-  // matrix pipe while this wave computes P of tile t on the VALU) and
-  // P V(t).  In the last iteration the score MFMAs read a stale K slot and
-  // their result is dropped.  Slot reuse: K(t+2) overwrites K(t), last read
-  // by the score MFMAs of iteration t-1; V(t+1) overwrites V(t-1), last read
-  // in iteration t-1; the barrier closing each iteration separates the two.
+  // Iteration t issues the loads of K(t+2) and V(t+1), masks tile t (and for
+  // an exact step updates the running max), then runs the score MFMAs of
+  // tile t+1 (on the matrix pipe while this wave computes P of tile t on the
+  // VALU) and P V(t).  In the last iteration the score MFMAs read a stale K
+  // slot and their result is dropped.  Slot reuse: K(t+2) overwrites K(t),
+  // last read by the score MFMAs of iteration t-1; V(t+1) overwrites V(t-1),
+  // last read in iteration t-1; the barrier closing each iteration separates
+  // the two.
   if (ntiles > 0) {
-    load_k(0);
-    load_v(0);
+    load_k(0, 0);
+    load_v(0, 0);
   }
-  if (ntiles > 1) load_k(1);
+  if (ntiles > 1) load_k(1, 1);
   wait_lds_dma();
   __syncthreads();
   f32x16 sa[BN / 32], sb[BN / 32];
   if (ntiles > 0) scores(0, sa);
-  auto step = [&](int t, f32x16* cur, f32x16* nxt) {
-    if (t + 2 < ntiles) load_k(t + 2);
-    if (t + 1 < ntiles) load_v(t + 1);
-    exp_pv(t, cur, nxt, prepare(t, cur));
-    // this wave's loads have landed; after the barrier every wave's have,
-    // and no wave reads slot K(t) / V(t) any more
+  // Step 0 loads K(2) into slot 0, which every wave has just read for
+  // scores(0): no wave may issue that load before all of them have their
+  // K(0) operands (each wave's reads complete before it reaches the
+  // barrier).  In later steps the barrier closing step t-1 orders the reads
+  // of slot par (scores(t), issued in step t-1) before the load into it.
+  __syncthreads();
+  // loads of K(t+2) into K slot par and V(t+1) into V slot par ^ 1
+  auto issue = [&](int t, int par) {
+    if (t + 2 < ntiles) load_k(t + 2, par);
+    if (t + 1 < ntiles) load_v(t + 1, par ^ 1);
+  };
+  // this wave's loads have landed; after the barrier every wave's have, and
+  // no wave reads slot K(t) / V(t) any more
+  auto close = [&]() {
     wait_lds_dma();
     __syncthreads();
   };
-  for (int t = 0; t < ntiles; t += 2) {
-    step(t, sa, sb);
-    if (t + 1 < ntiles) step(t + 1, sb, sa);
+  // ALiBi raises a row's max on nearly every tile while the keys approach
+  // the query (by slope * 64 per tile), so ALiBi steps stay exact: the
+  // rescale in registers is far cheaper than recomputing the tile.
+  constexpr bool kLazy = NORM == NORM_SOFTMAX && BIAS != BIAS_ALIBI;
+  if constexpr (kLazy) {
+    if (ntiles > 0) {
+      issue(0, 0);
+      step_exact(0, 0, sa, sb);
+      close();
+    }
+    for (int t = 1; t < ntiles; t += 2) {
+      issue(t, 1);
+      step_lazy(t, 1, sb, sa);
+      close();
+      if (t + 1 < ntiles) {
+        issue(t + 1, 0);
+        step_lazy(t + 1, 0, sa, sb);
+        close();
+      }
+    }
+  } else {
+    for (int t = 0; t < ntiles; t += 2) {
+      issue(t, 0);
+      step_exact(t, 0, sa, sb);
+      close();
+      if (t + 1 < ntiles) {
+        issue(t + 1, 1);
+        step_exact(t + 1, 1, sb, sa);
+        close();
+      }
+    }
   }
-
   // ---- epilogue -------------------------------------------------------------
   // this lane's 32 keys of every tile, plus the partner lane's 32
   float lt = lsum[0] + lsum[1];
