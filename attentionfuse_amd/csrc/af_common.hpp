@@ -410,4 +410,17 @@ struct RowsDma {
 // then publishes the whole stage).
 __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// ---------------------------------------------------------------------------
+// Entry e (wave-uniform) of one BlockMask row: list a, then list b.  The
+// lists are read through the constant address space, so the compiler loads
+// them with scalar loads (s_load_dword, counted by lgkmcnt).  Through a
+// generic pointer it used a vector load, and the s_waitcnt vmcnt that
+// consumed it also waited for every tile load into LDS still in flight: each
+// step of a block-sparse loop stalled until the previous tiles had landed.
+// ---------------------------------------------------------------------------
+typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+__device__ inline int bs_row_get(const int32_t* a, int na, const int32_t* b, int e) {
+  return e < na ? ((const_i32_ptr)a)[e] : ((const_i32_ptr)b)[e - na];
+}
+
 }  // namespace af

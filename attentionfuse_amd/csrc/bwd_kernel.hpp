@@ -369,7 +369,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   auto tile_m0 = [&](int t) -> int {
     if constexpr (MASK == MASK_BS) {
       const int e = t / bs_sub;
-      return bs_row[e] * p.bs_block_m + (t - e * bs_sub) * 32;
+      return bs_row_get(bs_row, bs_n, bs_row, e) * p.bs_block_m + (t - e * bs_sub) * 32;
     } else {
       return m_lo + 32 * t;
     }
@@ -562,7 +562,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   }
 
   int n_lo = 0, n_hi = p.Nkv, ntiles;
-  int bs_nfull = 0, bs_sub = 1;
+  int bs_nfull = 0, bs_npart = 0, bs_sub = 1;
   const int32_t* bs_full_row = nullptr;
   const int32_t* bs_part_row = nullptr;
   if constexpr (MASK == MASK_CAUSAL) {
@@ -577,17 +577,17 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   if constexpr (MASK == MASK_BS) {
     bs_sub = p.bs_block_n / 32;
     bs_nfull = p.bs_full_num[mb];
+    bs_npart = p.bs_part_num[mb];
     bs_full_row = p.bs_full_idx + mb * p.bs_full_rs;
     bs_part_row = p.bs_part_idx + mb * p.bs_part_rs;
-    ntiles = (bs_nfull + p.bs_part_num[mb]) * bs_sub;
+    ntiles = (bs_nfull + bs_npart) * bs_sub;
   } else {
     ntiles = n_hi > n_lo ? (n_hi - n_lo + 31) / 32 : 0;
   }
   auto tile_n0 = [&](int t) -> int {
     if constexpr (MASK == MASK_BS) {
       const int e = t / bs_sub;
-      const int blk = e < bs_nfull ? bs_full_row[e] : bs_part_row[e - bs_nfull];
-      return blk * p.bs_block_n + (t - e * bs_sub) * 32;
+      return bs_row_get(bs_full_row, bs_nfull, bs_part_row, e) * p.bs_block_n + (t - e * bs_sub) * 32;
     } else {
       return n_lo + 32 * t;
     }

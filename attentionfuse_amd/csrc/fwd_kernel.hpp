@@ -141,7 +141,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
 
   // ---- key-tile schedule ------------------------------------------------
   int n_lo = 0, n_hi = p.Nkv, ntiles;
-  int bs_nfull = 0, bs_sub = 1;
+  int bs_nfull = 0, bs_npart = 0, bs_sub = 1;
   const int32_t* bs_full_row = nullptr;
   const int32_t* bs_part_row = nullptr;
   if constexpr (MASK == MASK_CAUSAL) {
@@ -156,17 +156,17 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   if constexpr (MASK == MASK_BS) {
     bs_sub = p.bs_block_n / BN;
     bs_nfull = p.bs_full_num[mb];
+    bs_npart = p.bs_part_num[mb];
     bs_full_row = p.bs_full_idx + mb * p.bs_full_rs;
     bs_part_row = p.bs_part_idx + mb * p.bs_part_rs;
-    ntiles = (bs_nfull + p.bs_part_num[mb]) * bs_sub;
+    ntiles = (bs_nfull + bs_npart) * bs_sub;
   } else {
     ntiles = n_hi > n_lo ? (n_hi - n_lo + BN - 1) / BN : 0;
   }
   auto tile_n0 = [&](int t) -> int {
     if constexpr (MASK == MASK_BS) {
       const int e = t / bs_sub, s = t - e * bs_sub;
-      const int blk = e < bs_nfull ? bs_full_row[e] : bs_part_row[e - bs_nfull];
-      return blk * p.bs_block_n + s * BN;
+      return bs_row_get(bs_full_row, bs_nfull, bs_part_row, e) * p.bs_block_n + s * BN;
     } else {
       return n_lo + t * BN;
     }
