@@ -60,6 +60,17 @@ struct F16 {
     asm("v_fma_mix_f32 %0, %1, 1.0, 0 op_sel_hi:[1,0,0]" : "=v"(lo) : "v"(w));
     asm("v_fma_mix_f32 %0, %1, 1.0, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(hi) : "v"(w));
   }
+  // acc += w.lo + w.hi in fp32: one v_dot2_f32_f16 against (1, 1).  The
+  // products are exact and f16 denormals are kept, so the sum is the one two
+  // v_fma_mix_f32 give, in one instruction; it co-issues with the MFMAs of
+  // other waves like any other VALU instruction.
+  __device__ static inline void dot_pair(uint32_t w, float& acc) {
+    asm("v_dot2_f32_f16 %0, %1, %2, %0" : "+v"(acc) : "v"(w), "s"(0x3c003c00u));
+  }
+  // acc = w.lo + w.hi
+  __device__ static inline void dot_first(uint32_t w, float& acc) {
+    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(acc) : "v"(w), "s"(0x3c003c00u));
+  }
   // Call after the last add_pair into four sums, before ordinary code reads
   // them.  The compiler's hazard recognizer keeps dependent asm statements
   // two wait states apart, but it does not look at a compiler-generated
@@ -107,8 +118,17 @@ struct BF16 {
     lo = __builtin_bit_cast(float, w << 16);
     hi = __builtin_bit_cast(float, w & 0xffff0000u);
   }
-  // the sums are ordinary compiler-generated code
-  __device__ static inline void sums_ready(float&, float&, float&, float&) {}
+  // acc += w.lo + w.hi in fp32: one v_dot2_f32_bf16 against (1, 1)
+  __device__ static inline void dot_pair(uint32_t w, float& acc) {
+    asm("v_dot2_f32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(w), "s"(0x3f803f80u));
+  }
+  // acc = w.lo + w.hi
+  __device__ static inline void dot_first(uint32_t w, float& acc) {
+    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(acc) : "v"(w), "s"(0x3f803f80u));
+  }
+  __device__ static inline void sums_ready(float& a, float& b, float& c, float& d) {
+    asm volatile("s_nop 1" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+  }
 };
 
 // Unpack a 16-byte chunk into 8 floats / pack 8 floats into a chunk.

@@ -204,9 +204,10 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // sums add the rounded P that the P V MFMA uses, in fp32, so O = sum P V /
   // sum P stays a weighted mean of V even for one dominant key (the reference
   // sums the unrounded p, attnfuse/compiler/codegen.py:227, which is further
-  // from exact attention).  v_fma_mix (f16) or shift/mask + add (bf16)
-  // overlap with the MFMAs of other waves; v_dot2 on the packed P and
-  // all-ones MFMAs were measured to serialise with them.
+  // from exact attention).  One v_dot2_f32_{f16,bf16} against (1, 1) adds
+  // a packed pair exactly (f16 denormals kept) and co-issues with the MFMAs
+  // of other waves: 16 per tile, where v_fma_mix took 32 (f16) and
+  // shift/mask + add 64 (bf16).
   constexpr float kTau = 8.f;
   constexpr float kNegBig = -1.0e30f;
   f32x16 o[DB];
@@ -426,22 +427,23 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     }
   };
   // fp32 sums of the rounded P over this lane's 32 keys (the partner lane
-  // l ^ 32 holds the other 32): added into the two running chains ...
+  // l ^ 32 holds the other 32), one v_dot2 per packed pair: added into the
+  // two running chains ...
   auto add_rowsum = [&](const u32x4* pf) {
 #pragma unroll
     for (int kk = 0; kk < BN / 16; ++kk)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) E::add_pair(pf[kk][i], lsum[0], lsum[1]);
+      for (int i = 0; i < 4; ++i) E::dot_pair(pf[kk][i], lsum[i & 1]);
   };
   // ... or summed alone, over four chains, for the test of a lazy step
   auto tile_rowsum = [&](const u32x4* pf) -> float {
     float ts[4];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) E::first_pair(pf[kk][0], ts[2 * kk], ts[2 * kk + 1]);
+    for (int i = 0; i < 4; ++i) E::dot_first(pf[0][i], ts[i]);
 #pragma unroll
-    for (int kk = 0; kk < BN / 16; ++kk)
+    for (int kk = 1; kk < BN / 16; ++kk)
 #pragma unroll
-      for (int i = kk < 2 ? 1 : 0; i < 4; ++i) E::add_pair(pf[kk][i], ts[2 * (kk & 1)], ts[2 * (kk & 1) + 1]);
+      for (int i = 0; i < 4; ++i) E::dot_pair(pf[kk][i], ts[i]);
     E::sums_ready(ts[0], ts[1], ts[2], ts[3]);
     return (ts[0] + ts[1]) + (ts[2] + ts[3]);
   };
