@@ -261,7 +261,13 @@ __device__ inline void rope_pair(u32x4& lo, u32x4& hi, u32x4 clo, u32x4 slo,
                                  u32x4 chi, u32x4 shi);
 
 // fp16: written on half vectors so the compiler emits mixed-precision FMAs
-// (f16 operands, exact f32 product and sum, one rounding to f16).
+// (f16 operands, exact products, each sum rounded to f32), then each result
+// is rounded from f32 to f16.  The empty asm keeps the f32 rounding: without
+// it the compiler may fold the final FMA and the conversion into one
+// v_fma_mix{lo,hi}_f16, which rounds once, straight to f16, and then a key
+// rotated here can differ in its last bit from the same row rotated by the
+// forward's in-register query path (measured: it did, in a kernel that
+// rotates several rows per thread).
 template <>
 __device__ inline void rope_pair<F16>(u32x4& lo, u32x4& hi, u32x4 clo, u32x4 slo,
                                       u32x4 chi, u32x4 shi) {
@@ -273,8 +279,11 @@ __device__ inline void rope_pair<F16>(u32x4& lo, u32x4& hi, u32x4 clo, u32x4 slo
   for (int i = 0; i < 8; ++i) {
     const float a = __builtin_fmaf((float)xh[i], -(float)sl[i], 0.f);
     const float b = __builtin_fmaf((float)xl[i], (float)sh[i], 0.f);
-    ol[i] = (_Float16)__builtin_fmaf((float)xl[i], (float)cl[i], a);
-    oh[i] = (_Float16)__builtin_fmaf((float)xh[i], (float)ch[i], b);
+    float rl = __builtin_fmaf((float)xl[i], (float)cl[i], a);
+    float rh = __builtin_fmaf((float)xh[i], (float)ch[i], b);
+    asm("" : "+v"(rl), "+v"(rh));
+    ol[i] = (_Float16)rl;
+    oh[i] = (_Float16)rh;
   }
   lo = __builtin_bit_cast(u32x4, ol);
   hi = __builtin_bit_cast(u32x4, oh);

@@ -38,18 +38,41 @@ __device__ __forceinline__ void rope_row_chunk(const uint16_t* x, const uint16_t
   st16(out + dh, hi);
 }
 
-template <class E, int D>
+// A workgroup covers RPB consecutive positions n of one batch entry b and the
+// heads [h0, h0 + HG): thread j of a row rotates chunk pair j of position n
+// for each of those heads, so one cos/sin read serves HG rows and HG rows'
+// loads are in flight at once.  Workgroup index = (b * ceil(H/HG) + h0/HG) *
+// ceil(N/RPB) + n/RPB.
+template <class E, int D, int HG>
 __global__ void __launch_bounds__(256) rope_rows_kernel(const RopeRowsParams p) {
   constexpr int TPR = D / 16;          // threads per row
-  constexpr int RPB = 256 / TPR;       // rows per workgroup
-  const int tid = threadIdx.x;
-  const int64_t r = (int64_t)blockIdx.x * RPB + tid / TPR;
-  if (r >= p.rows) return;
-  const int n = (int)(r % p.N);
-  const int64_t bh = r / p.N;
-  const int hh = (int)(bh % p.H), b = (int)(bh / p.H);
-  rope_row_chunk<E, D>(p.x + b * p.xs[0] + hh * p.xs[1] + n * p.xs[2], p.cos + n * p.rs, p.sin + n * p.rs,
-                       p.out + r * D, tid % TPR);
+  constexpr int RPB = 256 / TPR;       // positions per workgroup
+  const int tid = threadIdx.x, j = tid % TPR;
+  const int nblocks = (p.N + RPB - 1) / RPB, hgroups = (p.H + HG - 1) / HG;
+  const int n = (int)(blockIdx.x % nblocks) * RPB + tid / TPR;
+  if (n >= p.N) return;
+  const int hb = (int)(blockIdx.x / nblocks);
+  const int h0 = (hb % hgroups) * HG, b = hb / hgroups;
+  const int dl = 8 * j, dh = dl + D / 2;
+  const uint16_t* x = p.x + b * p.xs[0] + h0 * p.xs[1] + n * p.xs[2];
+  uint16_t* out = p.out + (((int64_t)b * p.H + h0) * p.N + n) * D;
+  u32x4 lo[HG], hi[HG];
+#pragma unroll
+  for (int g = 0; g < HG; ++g)
+    if (h0 + g < p.H) {
+      lo[g] = ld16(x + g * p.xs[1] + dl);
+      hi[g] = ld16(x + g * p.xs[1] + dh);
+    }
+  const uint16_t* cr = p.cos + n * p.rs;
+  const uint16_t* sr = p.sin + n * p.rs;
+  const u32x4 clo = ld16(cr + dl), slo = ld16(sr + dl), chi = ld16(cr + dh), shi = ld16(sr + dh);
+#pragma unroll
+  for (int g = 0; g < HG; ++g)
+    if (h0 + g < p.H) {
+      rope_pair<E>(lo[g], hi[g], clo, slo, chi, shi);
+      st16(out + (int64_t)g * p.N * D + dl, lo[g]);
+      st16(out + (int64_t)g * p.N * D + dh, hi[g]);
+    }
 }
 
 }  // namespace af

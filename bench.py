@@ -56,7 +56,7 @@ C3 = dict(B=8, Hq=32, Hkv=8, N=32768, D=128)
 C4 = dict(B=4, H=12, N=4096, D=64)
 C5 = dict(B=1, Hq=32, Hkv=8, N=4096, D=128)
 # the kernels of one config-2 af_fwd call: keys rotated once, then attention
-FWD_KERNELS = ("rope_rows_kernel<af::F16, 64>", "fwd_kernel<af::F16, 64, 1, 0, 0, true, 4>")
+FWD_KERNELS = ("rope_rows_kernel<af::F16, 64, 4>", "fwd_kernel<af::F16, 64, 1, 0, 0, true, 4>")
 SETTLE_S = 0.3
 COPY_BYTES = 1 << 30
 

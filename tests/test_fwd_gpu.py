@@ -221,6 +221,28 @@ def test_config2_full_size_repeatable_and_exact():
     assert err <= TOL[torch.float16]
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,H,N,D", [(2, 5, 333, 64), (1, 3, 200, 128), (3, 12, 64, 32)])
+def test_rope_rounding_is_the_oracles(B, H, N, D, dtype):
+    """The fused RoPE forward equals, bit for bit, the plain causal forward
+    fed q~ = RoPE(q), k~ = RoPE(k) rotated by the oracle and rounded to the
+    input dtype.  Products of two 16-bit values are exact in fp32, so the
+    oracle's fp32 rotation rounds once per sum, as the kernels' FMAs do; a
+    kernel that rounds the rotated value straight to 16 bits (a fused
+    multiply-add-and-convert) differs in the last bit of some keys.  Five and
+    three heads leave a partial group for key rotations that handle several
+    heads per thread."""
+    Q, K, V = make(B, H, H, N, N, D, dtype, seed=3)
+    cos, sin = build_rope_cache(N, D, device="cuda", dtype=dtype)
+    out = af.attention(variant("rope_causal", H))(Q, K, V, cos=cos, sin=sin)
+    c, s = cos[0, 0].cpu().float(), sin[0, 0].cpu().float()
+    Qr = O.apply_rope(Q.cpu().float(), c, s).to(dtype).cuda()
+    Kr = O.apply_rope(K.cpu().float(), c, s).to(dtype).cuda()
+    plain = af.attention(variant("causal", H))(Qr, Kr, V)
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+
+
 @pytest.mark.parametrize("mask,N", [("causal", 256), ("causal", 333), ("sw", 300), ("full", 200),
                                     ("sw_causal", 300)])
 def test_tile_coverage_exact(mask, N):
