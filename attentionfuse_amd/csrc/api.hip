@@ -9,6 +9,7 @@
 
 #include "attnfuse_hip.h"
 #include "bwd_launch.hpp"
+#include "fwd_f32_kernel.hpp"
 #include "launch.hpp"
 #include "launch_decode.hpp"
 #include "validate.hpp"
@@ -36,9 +37,18 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-int check_key(const af_spec_key& k, bool allow_bs) {
-  if (k.dtype != AF_F16 && k.dtype != AF_BF16)
-    return fail(AF_ERR_UNSUPPORTED, "dtype %d: the gfx950 kernels take fp16 or bf16", k.dtype);
+// allow_f32: the entry point has an fp32 kernel (the dense / causal /
+// windowed forward; not block-sparse, decode or backward).
+int check_key(const af_spec_key& k, bool allow_bs, bool allow_f32 = false) {
+  if (k.dtype == AF_F32) {
+    if (!allow_f32)
+      return fail(AF_ERR_UNSUPPORTED, "dtype fp32: only the dense / causal / windowed forward (af_fwd) takes fp32; "
+                  "this entry point takes fp16 or bf16");
+    if (k.mask == AF_MASK_BLOCK_SPARSE)
+      return fail(AF_ERR_UNSUPPORTED, "dtype fp32: the block-sparse kernels take fp16 or bf16");
+  } else if (k.dtype != AF_F16 && k.dtype != AF_BF16) {
+    return fail(AF_ERR_UNSUPPORTED, "dtype %d: the gfx950 kernels take fp16, bf16 or (forward) fp32", k.dtype);
+  }
   if (k.head_dim != 32 && k.head_dim != 64 && k.head_dim != 128)
     return fail(AF_ERR_UNSUPPORTED, "head_dim %d: instantiated for 32, 64 and 128", k.head_dim);
   if (k.mask < 0 || k.mask > 4 || (!allow_bs && k.mask == AF_MASK_BLOCK_SPARSE))
@@ -133,7 +143,8 @@ bool slice_fits_u32(int64_t rows, int64_t row_stride, int d) {
 
 size_t fwd_workspace_bytes(const af_fwd_args& a) {
   if (!a.key.rope || a.batch <= 0 || a.heads_kv <= 0 || a.seqlen_kv <= 0 || a.key.head_dim <= 0) return 0;
-  const size_t bytes = (size_t)a.batch * a.heads_kv * a.seqlen_kv * a.key.head_dim * 2;
+  const size_t elem = a.key.dtype == AF_F32 ? 4 : 2;
+  const size_t bytes = (size_t)a.batch * a.heads_kv * a.seqlen_kv * a.key.head_dim * elem;
   return (bytes + 255) & ~size_t(255);
 }
 
@@ -206,6 +217,42 @@ int dispatch_fwd(FwdParams p, const af_fwd_args& a, int waves, void* workspace, 
   return AF_OK;
 }
 
+// fp32 forward: keys rotated once into the workspace with RoPE, then
+// fwd_f32_kernel over 128-row query blocks.
+int dispatch_fwd_f32(const af_fwd_args& a, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  if (a.coverage != nullptr)
+    return fail(AF_ERR_UNSUPPORTED, "tile-visit counters are kept by the fp16/bf16 kernels only");
+  FwdF32Params fp;
+  fp.f = make_fwd_params(&a, kF32BlockM);
+  fp.mask = a.key.mask;
+  fp.bias = a.key.bias;
+  fp.norm = a.key.norm;
+  fp.rope = a.key.rope;
+  FwdParams& p = fp.f;
+  if (!(p.scale > 0.f) || p.scale == INFINITY)
+    return fail(AF_ERR_BAD_ARG, "scale must be positive and finite (got %g)", (double)p.scale);
+  const int D = a.key.head_dim;
+  if (a.key.rope && a.seqlen_kv > 0) {
+    const size_t need = fwd_workspace_bytes(a);
+    if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+      return fail(AF_ERR_WORKSPACE, "forward with RoPE needs a %zu-byte workspace (16-byte aligned), got %zu", need,
+                  workspace_bytes);
+    const int64_t rows = (int64_t)a.batch * a.heads_kv * a.seqlen_kv;
+    launch_rope_f32(static_cast<const float*>(a.k), static_cast<float*>(workspace), static_cast<const float*>(a.cos),
+                    static_cast<const float*>(a.sin), a.k_stride, a.rope_stride[0], a.heads_kv, a.seqlen_kv, rows, D,
+                    s);
+    p.k = static_cast<const uint16_t*>(workspace);
+    p.ks[2] = D;
+    p.ks[1] = (int64_t)a.seqlen_kv * D;
+    p.ks[0] = (int64_t)a.heads_kv * a.seqlen_kv * D;
+  }
+  const dim3 grid((unsigned)p.n_mblocks * (unsigned)(p.B * p.Hq));
+  if (launch_fwd_f32(fp, D, grid, s) != 0) return fail(AF_ERR_UNSUPPORTED, "no fp32 forward for head_dim %d", D);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(AF_ERR_LAUNCH, "fp32 forward launch failed: %s", hipGetErrorString(e));
+  return AF_OK;
+}
+
 }  // namespace
 }  // namespace af
 
@@ -219,13 +266,18 @@ int af_abi_version(void) { return AF_ABI_VERSION; }
 
 int af_query(const af_spec_key* key) {
   if (key == nullptr) return 0;
-  return check_key(*key, true) == AF_OK ? 1 : 0;
+  return check_key(*key, true, true) == AF_OK ? 1 : 0;
 }
 
 int af_fwd_tile(const af_spec_key* key, int32_t* block_m, int32_t* block_n) {
   if (key == nullptr) return fail(AF_ERR_BAD_ARG, "key is NULL");
-  int rc = check_key(*key, true);
+  int rc = check_key(*key, true, true);
   if (rc) return rc;
+  if (key->dtype == AF_F32) {
+    if (block_m) *block_m = kF32BlockM;
+    if (block_n) *block_n = 32;
+    return AF_OK;
+  }
   if (block_m) *block_m = 32 * fwd_waves(*key);
   if (block_n) *block_n = kKeysPerStage;
   return AF_OK;
@@ -238,8 +290,9 @@ size_t af_fwd_workspace_bytes(const af_fwd_args* args) {
 int af_fwd(const af_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_fwd_common(a);
   if (rc) return rc;
-  if ((rc = check_key(a->key, false))) return rc;
+  if ((rc = check_key(a->key, false, true))) return rc;
   if (a->seqlen_q == 0) return AF_OK;
+  if (a->key.dtype == AF_F32) return dispatch_fwd_f32(*a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
   const int waves = fwd_waves(a->key);
   const FwdParams p = make_fwd_params(a, 32 * waves);
   return dispatch_fwd(p, *a, waves, workspace, workspace_bytes, static_cast<hipStream_t>(stream));

@@ -37,4 +37,11 @@ AF_DECLARE_ROPE(launch_rope_bf16_d64)
 AF_DECLARE_ROPE(launch_rope_bf16_d128)
 #undef AF_DECLARE_ROPE
 
+// fp32 forward and fp32 key rotation, defined in fwd_f32.hip; return -1 for
+// a head dim with no instantiation.
+struct FwdF32Params;
+int launch_fwd_f32(const FwdF32Params& p, int head_dim, dim3 grid, hipStream_t s);
+int launch_rope_f32(const float* x, float* out, const float* cs, const float* sn, const int64_t* xs, int64_t rs,
+                    int H, int N, int64_t rows, int head_dim, hipStream_t s);
+
 }  // namespace af

@@ -66,11 +66,29 @@ def test_query_and_tile():
     lib = N.lib()
     assert lib.af_query(N.SpecKeyC(0, 64, 1, 1, 0, 1)) == 1
     assert lib.af_query(N.SpecKeyC(1, 128, 3, 0, 0, 0)) == 1
-    assert lib.af_query(N.SpecKeyC(2, 64, 0, 0, 0, 0)) == 0      # fp32
+    assert lib.af_query(N.SpecKeyC(2, 64, 1, 1, 1, 1)) == 1      # fp32 forward
+    assert lib.af_query(N.SpecKeyC(2, 64, 3, 0, 0, 0)) == 0      # fp32 block-sparse
+    assert lib.af_query(N.SpecKeyC(3, 64, 0, 0, 0, 0)) == 0      # dtype
     assert lib.af_query(N.SpecKeyC(0, 80, 0, 0, 0, 0)) == 0      # head_dim
     bm, bn = C.c_int32(), C.c_int32()
     assert lib.af_fwd_tile(N.SpecKeyC(0, 64, 1, 0, 0, 0), C.byref(bm), C.byref(bn)) == 0
     assert (bm.value, bn.value) == (128, 64)
+    assert lib.af_fwd_tile(N.SpecKeyC(2, 64, 1, 0, 0, 0), C.byref(bm), C.byref(bn)) == 0
+    assert (bm.value, bn.value) == (128, 32)
+
+
+def test_fp32_outside_the_forward_is_rejected():
+    """fp32 has a forward kernel only: the backward, decode and block-sparse
+    entry points reject it with an error that names the dtypes they take."""
+    lib = N.lib()
+    a = N.DecodeArgsC()
+    a.key = N.SpecKeyC(2, 64, 0, 0, 0, 0)
+    a.batch, a.heads_q, a.heads_kv, a.seqlen_kv = 1, 4, 4, 64
+    a.q, a.k, a.v, a.o = 256, 256, 256, 256
+    for s in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
+        s[:] = (64 * 4 * 64, 64 * 64, 64, 1)
+    assert lib.af_decode(a, None, 0, None) == N.AF_ERR_UNSUPPORTED
+    assert "fp16 or bf16" in N.last_error()
 
 
 def test_argument_errors_need_no_gpu():
@@ -103,8 +121,15 @@ def test_argument_errors_need_no_gpu():
     a.heads_kv = 4
     a.seqlen_kv = 32
     assert lib.af_fwd(a, None, 0, None) == N.AF_ERR_BAD_ARG        # causal needs Nq == Nkv
+    a.key = N.SpecKeyC(3, 64, 0, 0, 0, 0)
+    assert lib.af_fwd(a, None, 0, None) == N.AF_ERR_UNSUPPORTED       # no such dtype
     a.key = N.SpecKeyC(2, 64, 0, 0, 0, 0)
-    assert lib.af_fwd(a, None, 0, None) == N.AF_ERR_UNSUPPORTED
+    assert lib.af_fwd(a, None, 0, None) == N.AF_ERR_BAD_ARG           # fp32 taken; scale 0 refused
+    assert "scale" in N.last_error()
+    a.key = N.SpecKeyC(2, 64, 0, 0, 0, 1)                               # fp32 k~ is 4 bytes a value
+    a.seqlen_kv = 64
+    assert lib.af_fwd_workspace_bytes(a) == 1 * 4 * 64 * 64 * 4
+    a.seqlen_kv = 32
     # fused RoPE needs the rotated-key workspace: B*Hkv*Nkv*D*2 bytes, rounded
     # up to 256; refused before any launch when it is missing or too small
     a.key = N.SpecKeyC(0, 64, 0, 0, 0, 1)
