@@ -1,7 +1,7 @@
 """Benchmark of the fused-attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--no-cpu] [--no-decode] [--no-alibi] [--no-train]
+                    [--no-cpu] [--no-decode] [--no-alibi] [--no-train] [--no-fp32]
     python bench.py --copy-calibration      # plain copy, for HBM counters
 
 A step is one fused forward over config 2 of the benchmark configs: causal +
@@ -18,6 +18,9 @@ HBM, every step exactly one kernel launch.  The same line carries
   (profiles/hbm_traffic_*.txt, scaled by a plain copy of known size), or
   null when that summary is absent;
 * ``alibi`` -- the same forward with ALiBi added (config 2 as written);
+* ``fp32`` -- the same forward (causal + RoPE, no ALiBi) on fp32 inputs,
+  which compute on the fp32 matrix cores, against their 157.3 TFLOP/s dense
+  peak;
 * ``decode`` -- config 3 (Llama-3-8B GQA decode, bf16, B=8, H_q=32, H_kv=8,
   D=128, cache 32768): algorithmic bytes K+V+Q+O = 1,073,872,896 per call
   over kernel time (split + combine), against 8 TB/s; two K/V cache copies
@@ -49,6 +52,7 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_FP16_TFLOPS = 2500.0      # MI355X dense fp16/bf16 MFMA, published
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, published
+PEAK_FP32_TFLOPS = 157.3       # MI355X dense fp32 MFMA, published
 
 C1 = dict(B=1, H=12, N=512, D=64)
 C2 = dict(B=4, H=12, N=4096, D=64)
@@ -101,7 +105,7 @@ def _time_launch(launch, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
-def bench_forward(steps, warmup, alibi: bool, settle_s: float = 0.0):
+def bench_forward(steps, warmup, alibi: bool, settle_s: float = 0.0, dtype=None):
     import torch
 
     import attnfuse as af
@@ -109,12 +113,13 @@ def bench_forward(steps, warmup, alibi: bool, settle_s: float = 0.0):
     from attentionfuse_amd.runtime.prepared import prepare_attention
 
     dev = torch.device("cuda:0")
+    dtype = torch.float16 if dtype is None else dtype
     B, H, N, D = C2["B"], C2["H"], C2["N"], C2["D"]
     g = torch.Generator(device=dev).manual_seed(0)
-    Q = torch.randn(B, H, N, D, generator=g, device=dev, dtype=torch.float16)
-    K = torch.randn(B, H, N, D, generator=g, device=dev, dtype=torch.float16)
-    V = torch.randn(B, H, N, D, generator=g, device=dev, dtype=torch.float16)
-    cos, sin = build_rope_cache(N, D, device=dev, dtype=torch.float16)
+    Q = torch.randn(B, H, N, D, generator=g, device=dev, dtype=dtype)
+    K = torch.randn(B, H, N, D, generator=g, device=dev, dtype=dtype)
+    V = torch.randn(B, H, N, D, generator=g, device=dev, dtype=dtype)
+    cos, sin = build_rope_cache(N, D, device=dev, dtype=dtype)
     if alibi:
         fn = af.attention(lambda Q, K, V: af.softmax(af.causal(af.alibi(af.rope(Q, K), H))) @ V)
     else:
@@ -356,6 +361,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-alibi", action="store_true")
+    ap.add_argument("--no-fp32", action="store_true")
     ap.add_argument("--no-train", action="store_true",
                     help="skip the fwd+bwd configs 4 and 5")
     ap.add_argument("--copy-calibration", action="store_true")
@@ -417,6 +423,14 @@ def main():
                          "ms": round(ms_alibi, 5), "tflops": round(tflops_alibi, 3),
                          "frac": round(tflops_alibi / PEAK_FP16_TFLOPS, 4),
                          "slopes": "2^(-8(h+1)/H), h=0..11 (config 2 as written)"}
+    if not args.no_fp32:
+        import torch
+        ms_f32, _ = bench_forward(args.steps, args.warmup, alibi=False, dtype=torch.float32)
+        tflops_f32 = flops / (ms_f32 * 1e-3) / 1e12
+        line["fp32"] = {"workload": "config 2's causal+RoPE forward on fp32 inputs, B=4 H=12 N=4096 D=64",
+                        "ms": round(ms_f32, 5), "tflops": round(tflops_f32, 3), "bound": "mfma",
+                        "peak": PEAK_FP32_TFLOPS,
+                        "frac": round(tflops_f32 / PEAK_FP32_TFLOPS, 4)}
     if not args.no_decode:
         ms_dec = bench_decode(args.steps, args.warmup)
         nbytes = decode_bytes(**{k: C3[k] for k in ("B", "Hq", "Hkv", "N", "D")})

@@ -66,7 +66,7 @@ typedef enum af_norm { AF_NORM_SOFTMAX = 0, AF_NORM_RELU = 1 } af_norm;
 /* Specialisation key: replaces the reference's Triton constexpr record
  * (attnfuse/compiler/codegen.py:391-404; attnfuse/ir/tiled.py:52-81). */
 typedef struct af_spec_key {
-  int32_t dtype;     /* af_dtype                  */
+  int32_t dtype;     /* af_dtype; AF_F32: af_fwd only (not block-sparse) */
   int32_t head_dim;  /* instantiated: 32, 64, 128 (af_query) */
   int32_t mask;      /* af_mask                   */
   int32_t bias;      /* af_bias                   */
@@ -120,6 +120,9 @@ typedef struct af_fwd_args {
  * re-rotating every key tile in every query block; 0 without RoPE (the
  * workspace may then be NULL). */
 size_t af_fwd_workspace_bytes(const af_fwd_args* args);
+/* fp16 / bf16: 16-bit MFMAs with fp32 accumulation.  AF_F32: q, k, v, o,
+ * tables and bias in fp32, every product in fp32 on the fp32 MFMAs (the
+ * reference's Triton dots run fp32 inputs in TF32); coverage must be NULL. */
 int af_fwd(const af_fwd_args* args, void* workspace, size_t workspace_bytes,
            void* stream);
 
