@@ -38,11 +38,12 @@ int fail(int code, const char* fmt, ...) {
 }
 
 // allow_f32: the entry point has an fp32 kernel (the dense / causal /
-// windowed forward; not block-sparse, decode or backward).
+// windowed forward; af_bwd checks its own keys; decode and block-sparse
+// have none).
 int check_key(const af_spec_key& k, bool allow_bs, bool allow_f32 = false) {
   if (k.dtype == AF_F32) {
     if (!allow_f32)
-      return fail(AF_ERR_UNSUPPORTED, "dtype fp32: only the dense / causal / windowed forward (af_fwd) takes fp32; "
+      return fail(AF_ERR_UNSUPPORTED, "dtype fp32: af_fwd and af_bwd take fp32 (dense / causal / windowed masks); "
                   "this entry point takes fp16 or bf16");
     if (k.mask == AF_MASK_BLOCK_SPARSE)
       return fail(AF_ERR_UNSUPPORTED, "dtype fp32: the block-sparse kernels take fp16 or bf16");

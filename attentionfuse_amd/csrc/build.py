@@ -40,6 +40,7 @@ UNITS = [
     ("decode", "decode_inst.hip", []),
     ("bwd", "bwd.hip", []),
     ("fwd_f32", "fwd_f32.hip", []),
+    ("bwd_f32", "bwd_f32.hip", []),
 ] + [
     (f"{kind}_{dt}_d{d}", f"{kind}_inst.hip", [f"-DAF_DT={code}", f"-DAF_D={d}"])
     for kind in ("fwd", "bwd")

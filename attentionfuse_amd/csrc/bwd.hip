@@ -27,14 +27,16 @@ BwdWorkspace bwd_workspace_layout(const af_bwd_args& a) {
   const size_t rows_q = (size_t)a.batch * a.heads_q * a.seqlen_q;
   const size_t rows_k = (size_t)a.batch * a.heads_kv * a.seqlen_kv;
   w.ld = 0;
+  const size_t elem = a.key.dtype == AF_F32 ? 4 : 2;
   w.total = up(rows_q * 2 * sizeof(float));
   if (a.key.rope) {
     w.qr = w.total;
-    w.total += up(rows_q * a.key.head_dim * 2);
+    w.total += up(rows_q * a.key.head_dim * elem);
     w.kr = w.total;
-    w.total += up(rows_k * a.key.head_dim * 2);
+    w.total += up(rows_k * a.key.head_dim * elem);
   }
-  w.g_split = bwd_group_split(a);
+  // the fp32 dK/dV kernel sums its whole GQA group itself
+  w.g_split = a.key.dtype == AF_F32 ? 1 : bwd_group_split(a);
   if (w.g_split > 1) {
     w.dkp = w.total;
     w.total += up((size_t)w.g_split * rows_k * a.key.head_dim * 4);
@@ -56,7 +58,11 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
             hipStream_t stream) {
   if (a == nullptr) return bad(AF_ERR_BAD_ARG, "args is NULL");
   const af_spec_key& k = a->key;
-  if (k.dtype != AF_F16 && k.dtype != AF_BF16) return bad(AF_ERR_UNSUPPORTED, "backward takes fp16 or bf16");
+  const bool f32 = k.dtype == AF_F32;
+  if (k.dtype != AF_F16 && k.dtype != AF_BF16 && !f32)
+    return bad(AF_ERR_UNSUPPORTED, "backward takes fp16, bf16 or fp32");
+  if (f32 && k.mask == AF_MASK_BLOCK_SPARSE)
+    return bad(AF_ERR_UNSUPPORTED, "the block-sparse backward takes fp16 or bf16");
   if (!head_dim_supported(k.head_dim)) return bad(AF_ERR_UNSUPPORTED, "backward head_dim must be 32, 64 or 128");
   if (k.mask < 0 || k.mask > 4) return bad(AF_ERR_UNSUPPORTED, "unknown mask kind");
   if (k.bias != AF_BIAS_NONE && k.bias != AF_BIAS_ALIBI)
@@ -94,9 +100,9 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   auto fits = [&](int64_t rows, int64_t stride) {
     return rows <= 0 || ((rows - 1) * stride + k.head_dim) * 2 < (int64_t(1) << 32);
   };
-  if (!fits(a->seqlen_q, a->q_stride[2]) || !fits(a->seqlen_q, a->do_stride[2]) ||
-      !fits(a->seqlen_kv, a->k_stride[2]) || !fits(a->seqlen_kv, a->v_stride[2]) ||
-      (k.rope && !fits(a->rope_len, a->rope_stride[0])))
+  if (!f32 && (!fits(a->seqlen_q, a->q_stride[2]) || !fits(a->seqlen_q, a->do_stride[2]) ||
+               !fits(a->seqlen_kv, a->k_stride[2]) || !fits(a->seqlen_kv, a->v_stride[2]) ||
+               (k.rope && !fits(a->rope_len, a->rope_stride[0]))))
     return bad(AF_ERR_UNSUPPORTED, "a (batch, head) slice spans 4 GiB or more");
   const BwdWorkspace wl = bwd_workspace_layout(*a);
   const size_t need = wl.total;
@@ -198,6 +204,15 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
     p.bs_block_n = bm->block_n;
   }
   if (a->seqlen_q == 0 && a->seqlen_kv == 0) return AF_OK;
+  if (f32) {
+    if (launch_bwd_f32(p, *a, stream) != 0) return bad(AF_ERR_UNSUPPORTED, "no fp32 backward for this head dim");
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+      set_error("fp32 backward launch failed: %s", hipGetErrorString(e));
+      return AF_ERR_LAUNCH;
+    }
+    return AF_OK;
+  }
   const int BK = 32 * g.waves_kv, BMq = 32 * g.waves_q;
   p.n_kblocks = (a->seqlen_kv + BK - 1) / BK;
   p.n_qblocks = (a->seqlen_q + BMq - 1) / BMq;

@@ -1,0 +1,43 @@
+// Launch sequence of the fp32 backward (bwd_f32_kernel.hpp): RoPE of q and k
+// into the workspace, the per-row prep, then the dK/dV and dQ kernels.
+#include "attnfuse_hip.h"
+#include "bwd_f32_kernel.hpp"
+#include "launch.hpp"
+
+namespace af {
+
+template <int D>
+static void launch_bwd_f32_d(BwdParams p, int mask, int bias, int rope, hipStream_t s) {
+  const int64_t rows_q = (int64_t)p.B * p.Hq * p.Nq;
+  if (rows_q > 0)
+    hipLaunchKernelGGL((bwd_prep_f32_kernel<D>), dim3((unsigned)((rows_q + 255) / 256)), dim3(256), 0, s, p);
+  const unsigned grid_kv = (unsigned)(p.n_kblocks * p.B * p.Hkv);
+  if (grid_kv > 0)
+    hipLaunchKernelGGL((bwd_dkv_f32_kernel<D>), dim3(grid_kv), dim3(kBwdF32Waves * 64), 0, s, p, mask, bias, rope);
+  const unsigned grid_q = (unsigned)(p.n_qblocks * p.B * p.Hq);
+  if (grid_q > 0)
+    hipLaunchKernelGGL((bwd_dq_f32_kernel<D>), dim3(grid_q), dim3(kBwdF32Waves * 64), 0, s, p, mask, bias, rope);
+}
+
+int launch_bwd_f32(BwdParams p, const af_bwd_args& a, hipStream_t s) {
+  const int D = a.key.head_dim;
+  p.n_kblocks = (a.seqlen_kv + kBwdF32Block - 1) / kBwdF32Block;
+  p.n_qblocks = (a.seqlen_q + kBwdF32Block - 1) / kBwdF32Block;
+  if (a.key.rope) {
+    // q~ and k~ (fp32, contiguous) into the workspace copies p.qr / p.kr
+    launch_rope_f32(static_cast<const float*>(a.q), reinterpret_cast<float*>(p.qr), static_cast<const float*>(a.cos),
+                    static_cast<const float*>(a.sin), a.q_stride, a.rope_stride[0], a.heads_q, a.seqlen_q,
+                    (int64_t)a.batch * a.heads_q * a.seqlen_q, D, s);
+    launch_rope_f32(static_cast<const float*>(a.k), reinterpret_cast<float*>(p.kr), static_cast<const float*>(a.cos),
+                    static_cast<const float*>(a.sin), a.k_stride, a.rope_stride[0], a.heads_kv, a.seqlen_kv,
+                    (int64_t)a.batch * a.heads_kv * a.seqlen_kv, D, s);
+  }
+  switch (D) {
+    case 32: launch_bwd_f32_d<32>(p, a.key.mask, a.key.bias, a.key.rope, s); return 0;
+    case 64: launch_bwd_f32_d<64>(p, a.key.mask, a.key.bias, a.key.rope, s); return 0;
+    case 128: launch_bwd_f32_d<128>(p, a.key.mask, a.key.bias, a.key.rope, s); return 0;
+  }
+  return -1;
+}
+
+}  // namespace af

@@ -1,0 +1,381 @@
+// fp32 backward: dQ, dK, dV of softmax attention for fp32 inputs, every
+// product in fp32 on the fp32 matrix cores (v_mfma_f32_32x32x2_f32).
+//
+// The reference runs fp32 backward through Triton dots in TF32, with dQ's
+// product cast to bf16 (attnfuse/compiler/codegen_backward.py:287-297), and
+// tests it at 2e-2 (tests/test_backward.py:30-33).  The structure follows
+// the fp32 forward (fwd_f32_kernel.hpp):
+//
+//   bwd_prep_f32_kernel  per query row: delta = sum_d dO O and L log2(e)
+//                        (0 for a row that sees no key) into the workspace.
+//   bwd_dkv_f32_kernel   a wave owns 32 keys; its k~ and v rows sit in LDS.
+//                        For every query head of its group and 32-row query
+//                        tile: S = q~ k~^T and dP = dO v^T with queries as
+//                        the MFMA rows, P and dS from the saved L and delta,
+//                        dV += P^T dO, dK += dS^T q~.  Register r of lane l
+//                        holds query 8(r/4) + 4h + (r mod 4) of key l mod 32
+//                        (h = l / 32), which is the query the A operand of
+//                        the r-th dV / dK MFMA needs from that lane.
+//   bwd_dq_f32_kernel    a wave owns 32 queries; its q~ and dO rows sit in
+//                        LDS.  Per 32-key tile: S^T and dP^T with keys as
+//                        the MFMA rows, dS^T, dQ^T += k~^T dS^T.
+//
+// Output block c, row m of dV, dK and dQ^T holds d = (D/32) m + c, so a
+// lane's operand reads and stores are D/32 consecutive floats.  With RoPE
+// the rotated-space gradients are rotated back before the store:
+// dx[d] = g[d] cos[d] + g[d + D/2] sin[d + D/2],
+// dx[d + D/2] = g[d + D/2] cos[d + D/2] - g[d] sin[d].
+#pragma once
+
+#include "af_common.hpp"
+#include "bwd_kernel.hpp"
+#include "fwd_f32_kernel.hpp"
+
+namespace af {
+
+constexpr int kBwdF32Waves = 4;
+constexpr int kBwdF32Block = 32 * kBwdF32Waves;
+
+// One thread per query row r = (b H_q + h) N_q + n.
+template <int D>
+__global__ void __launch_bounds__(256) bwd_prep_f32_kernel(const BwdParams p) {
+  const int64_t rows = (int64_t)p.B * p.Hq * p.Nq;
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  const int n = (int)(r % p.Nq);
+  const int64_t bh = r / p.Nq;
+  const int hq = (int)(bh % p.Hq), b = (int)(bh / p.Hq);
+  const float* o = reinterpret_cast<const float*>(p.o) + b * p.os[0] + hq * p.os[1] + (int64_t)n * p.os[2];
+  const float* g = reinterpret_cast<const float*>(p.dout) + b * p.dos[0] + hq * p.dos[1] + (int64_t)n * p.dos[2];
+  float delta = 0.f;
+#pragma unroll
+  for (int d = 0; d < D; d += 4) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(o + d);
+    const f32x4 c = *reinterpret_cast<const f32x4*>(g + d);
+    delta += a[0] * c[0] + a[1] * c[1] + a[2] * c[2] + a[3] * c[3];
+  }
+  const float L = p.lse[b * p.ls[0] + hq * p.ls[1] + (int64_t)n * p.ls[2]];
+  p.ld[2 * r] = L == -INFINITY ? 0.f : L * kLog2e;
+  p.ld[2 * r + 1] = delta;
+}
+
+// Visibility of key j to query i under the dense / causal / windowed masks.
+__device__ __forceinline__ bool f32_visible(int mask, int window, int i, int j) {
+  if (mask == MASK_CAUSAL) return j <= i;
+  if (mask == MASK_SW) return abs(i - j) < window;
+  if (mask == MASK_CSW) return j <= i && j > i - window;
+  return true;
+}
+
+// Rotate-back of a rotated-space gradient pair (lo = d < D/2, hi = d + D/2).
+__device__ __forceinline__ void f32_rope_back(float& lo, float& hi, float clo, float slo, float chi, float shi) {
+  const float a = lo * clo + hi * shi;
+  const float b = hi * chi - lo * slo;
+  lo = a;
+  hi = b;
+}
+
+template <int D>
+__global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const BwdParams p, int mask, int bias,
+                                                                         int rope) {
+  constexpr int DH = D / 2, DC = D / 32, KP = D + 4;
+  typedef typename F32Vec<DC>::T VecC;
+  __shared__ __attribute__((aligned(16))) float kl[kBwdF32Waves][32][KP];
+  __shared__ __attribute__((aligned(16))) float vl[kBwdF32Waves][32][KP];
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int col = lane & 31, h = lane >> 5;
+  const int nbh = p.B * p.Hkv;
+  const int kb = (int)(blockIdx.x / nbh), bh = (int)(blockIdx.x % nbh);
+  const int b = bh / p.Hkv, hk = bh % p.Hkv;
+  const int k0 = kb * kBwdF32Block + w * 32;
+
+  const float* kt = reinterpret_cast<const float*>(p.kt) + b * p.kts[0] + hk * p.kts[1];
+  const float* vg = reinterpret_cast<const float*>(p.v) + b * p.vs[0] + hk * p.vs[1];
+  for (int idx = lane; idx < 32 * (D / 4); idx += 64) {
+    const int r = idx / (D / 4), c4 = (idx % (D / 4)) * 4;
+    const int n = k0 + r;
+    f32x4 kv4 = {0.f, 0.f, 0.f, 0.f}, vv4 = {0.f, 0.f, 0.f, 0.f};
+    if (n < p.Nkv) {
+      kv4 = *reinterpret_cast<const f32x4*>(kt + (int64_t)n * p.kts[2] + c4);
+      vv4 = *reinterpret_cast<const f32x4*>(vg + (int64_t)n * p.vs[2] + c4);
+    }
+    *reinterpret_cast<f32x4*>(&kl[w][r][c4]) = kv4;
+    *reinterpret_cast<f32x4*>(&vl[w][r][c4]) = vv4;
+  }
+  __syncthreads();
+  if (k0 >= p.Nkv) return;
+
+  // query tiles that can see one of keys [k0, k0 + 32)
+  int q_lo = 0, q_hi = p.Nq;
+  if (mask == MASK_CAUSAL) {
+    q_lo = k0;
+  } else if (mask == MASK_SW) {
+    q_lo = max(0, k0 - p.window + 1);
+    q_hi = min(q_hi, k0 + 31 + p.window);
+  } else if (mask == MASK_CSW) {
+    q_lo = k0;
+    q_hi = min(q_hi, k0 + 31 + p.window);
+  }
+  q_lo &= ~31;
+
+  const float zc = p.scale * kLog2e;
+  const int key = k0 + col;  // this lane's key in S and dP
+  f32x16 dk[DC], dv[DC];
+#pragma unroll
+  for (int c = 0; c < DC; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dk[c][r] = dv[c][r] = 0.f;
+
+  for (int gi = 0; gi < p.G; ++gi) {
+    const int hq = hk * p.G + gi;
+    const float slope = bias == BIAS_ALIBI ? p.slopes[hq] * kLog2e : 0.f;
+    const float* qt = reinterpret_cast<const float*>(p.qt) + b * p.qts[0] + hq * p.qts[1];
+    const float* dog = reinterpret_cast<const float*>(p.dout) + b * p.dos[0] + hq * p.dos[1];
+    const float* ld = p.ld + 2 * ((int64_t)(b * p.Hq + hq) * p.Nq);
+    for (int q0 = q_lo; q0 < q_hi; q0 += 32) {
+      // S and dP: queries q0 + (l mod 32) as the A rows, d paired across halves
+      const int qa = min(q0 + col, p.Nq - 1);
+      const float* qrow = qt + (int64_t)qa * p.qts[2] + h * DH;
+      const float* grow = dog + (int64_t)qa * p.dos[2] + h * DH;
+      f32x16 s, dp;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+#pragma unroll
+      for (int j = 0; j < DH / 4; ++j) {
+        const f32x4 qa4 = *reinterpret_cast<const f32x4*>(qrow + 4 * j);
+        const f32x4 ka4 = *reinterpret_cast<const f32x4*>(&kl[w][col][h * DH + 4 * j]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(qa4[e], ka4[e], s, 0, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < DH / 4; ++j) {
+        const f32x4 ga4 = *reinterpret_cast<const f32x4*>(grow + 4 * j);
+        const f32x4 va4 = *reinterpret_cast<const f32x4*>(&vl[w][col][h * DH + 4 * j]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dp = __builtin_amdgcn_mfma_f32_32x32x2f32(ga4[e], va4[e], dp, 0, 0, 0);
+      }
+      // P and dS of query q0 + 8(r/4) + 4h + (r mod 4), key k0 + col
+      float pr[16], ds[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qi = q0 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const f32x2 l2 = *reinterpret_cast<const f32x2*>(ld + 2 * min(qi, p.Nq - 1));
+        float x = s[r] * zc - l2[0];
+        if (bias == BIAS_ALIBI) x -= slope * (float)abs(qi - key);
+        const bool vis = qi < p.Nq && key < p.Nkv && f32_visible(mask, p.window, qi, key);
+        pr[r] = vis ? __builtin_amdgcn_exp2f(x) : 0.f;
+        ds[r] = pr[r] * (dp[r] - l2[1]);
+      }
+      // dV += P^T dO and dK += dS^T q~: B operands are rows of dO / q~ at the
+      // queries of register i, D/32 consecutive d per lane
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int qi = min(q0 + 8 * (i >> 2) + 4 * h + (i & 3), p.Nq - 1);
+        const VecC gv = *reinterpret_cast<const VecC*>(dog + (int64_t)qi * p.dos[2] + DC * col);
+        const VecC qv = *reinterpret_cast<const VecC*>(qt + (int64_t)qi * p.qts[2] + DC * col);
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+          float gc, qc;
+          if constexpr (DC == 1) {
+            gc = gv;
+            qc = qv;
+          } else {
+            gc = gv[c];
+            qc = qv[c];
+          }
+          dv[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(pr[i], gc, dv[c], 0, 0, 0);
+          dk[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[i], qc, dk[c], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // dK (scaled, rotated back with RoPE) and dV rows k0 + 8(r/4) + 4h + (r mod 4)
+#pragma unroll
+  for (int c = 0; c < DC; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dk[c][r] *= p.scale;
+  if (rope) {
+    // d = DC col + c; its rotate-half partner d +- D/2 is lane col ^ 16
+    const bool lo = col < 16;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = min(k0 + 8 * (r >> 2) + 4 * h + (r & 3), p.Nkv - 1);
+      const float* cr = reinterpret_cast<const float*>(p.cos) + (int64_t)kr * p.rs[0];
+      const float* sr = reinterpret_cast<const float*>(p.sin) + (int64_t)kr * p.rs[0];
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        const float g = dk[c][r];
+        const float gp = __shfl_xor(g, 16, 64);
+        const int dl = lo ? DC * col + c : DC * col + c - DH;
+        float l = lo ? g : gp, hh = lo ? gp : g;
+        f32_rope_back(l, hh, cr[dl], sr[dl], cr[dl + DH], sr[dl + DH]);
+        dk[c][r] = lo ? l : hh;
+      }
+    }
+  }
+  float* dkg = reinterpret_cast<float*>(p.dk) + b * p.dks[0] + hk * p.dks[1];
+  float* dvg = reinterpret_cast<float*>(p.dv) + b * p.dvs[0] + hk * p.dvs[1];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int kr = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
+    if (kr >= p.Nkv) continue;
+    VecC a, v;
+    if constexpr (DC == 1) {
+      a = dk[0][r];
+      v = dv[0][r];
+    } else {
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        a[c] = dk[c][r];
+        v[c] = dv[c][r];
+      }
+    }
+    *reinterpret_cast<VecC*>(dkg + (int64_t)kr * p.dks[2] + DC * col) = a;
+    *reinterpret_cast<VecC*>(dvg + (int64_t)kr * p.dvs[2] + DC * col) = v;
+  }
+}
+
+template <int D>
+__global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dq_f32_kernel(const BwdParams p, int mask, int bias,
+                                                                        int rope) {
+  constexpr int DH = D / 2, DC = D / 32, QP = D + 4;
+  typedef typename F32Vec<DC>::T VecC;
+  __shared__ __attribute__((aligned(16))) float ql[kBwdF32Waves][32][QP];
+  __shared__ __attribute__((aligned(16))) float gl[kBwdF32Waves][32][QP];
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int col = lane & 31, h = lane >> 5;
+  const int nbh = p.B * p.Hq;
+  int mb = (int)(blockIdx.x / nbh);
+  const int bh = (int)(blockIdx.x % nbh);
+  if (mask == MASK_CAUSAL || mask == MASK_CSW) mb = p.n_qblocks - 1 - mb;
+  const int b = bh / p.Hq, hq = bh % p.Hq, hk = hq / p.G;
+  const int q0 = mb * kBwdF32Block + w * 32;
+  const int qrow = q0 + col;
+
+  const float* qt = reinterpret_cast<const float*>(p.qt) + b * p.qts[0] + hq * p.qts[1];
+  const float* dog = reinterpret_cast<const float*>(p.dout) + b * p.dos[0] + hq * p.dos[1];
+  for (int idx = lane; idx < 32 * (D / 4); idx += 64) {
+    const int r = idx / (D / 4), c4 = (idx % (D / 4)) * 4;
+    const int n = q0 + r;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f}, g = {0.f, 0.f, 0.f, 0.f};
+    if (n < p.Nq) {
+      a = *reinterpret_cast<const f32x4*>(qt + (int64_t)n * p.qts[2] + c4);
+      g = *reinterpret_cast<const f32x4*>(dog + (int64_t)n * p.dos[2] + c4);
+    }
+    *reinterpret_cast<f32x4*>(&ql[w][r][c4]) = a;
+    *reinterpret_cast<f32x4*>(&gl[w][r][c4]) = g;
+  }
+  __syncthreads();
+  if (q0 >= p.Nq) return;
+
+  int n_lo = 0, n_hi = p.Nkv;
+  if (mask == MASK_CAUSAL) {
+    n_hi = min(n_hi, q0 + 32);
+  } else if (mask == MASK_SW) {
+    n_lo = max(0, q0 - p.window + 1);
+    n_hi = min(n_hi, q0 + 31 + p.window);
+  } else if (mask == MASK_CSW) {
+    n_lo = max(0, q0 - p.window + 1);
+    n_hi = min(n_hi, q0 + 32);
+  }
+  n_lo &= ~31;
+
+  const float zc = p.scale * kLog2e;
+  const float slope = bias == BIAS_ALIBI ? p.slopes[hq] * kLog2e : 0.f;
+  const f32x2 l2 = *reinterpret_cast<const f32x2*>(p.ld + 2 * ((int64_t)(b * p.Hq + hq) * p.Nq + min(qrow, p.Nq - 1)));
+  const float* kt = reinterpret_cast<const float*>(p.kt) + b * p.kts[0] + hk * p.kts[1];
+  const float* vg = reinterpret_cast<const float*>(p.v) + b * p.vs[0] + hk * p.vs[1];
+
+  f32x16 dq[DC];
+#pragma unroll
+  for (int c = 0; c < DC; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[c][r] = 0.f;
+
+  for (int n0 = n_lo; n0 < n_hi; n0 += 32) {
+    const int ka = min(n0 + col, p.Nkv - 1);
+    const float* krow = kt + (int64_t)ka * p.kts[2] + h * DH;
+    const float* vrow = vg + (int64_t)ka * p.vs[2] + h * DH;
+    f32x16 s, dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < DH / 4; ++j) {
+      const f32x4 k4 = *reinterpret_cast<const f32x4*>(krow + 4 * j);
+      const f32x4 q4 = *reinterpret_cast<const f32x4*>(&ql[w][col][h * DH + 4 * j]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(k4[e], q4[e], s, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < DH / 4; ++j) {
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(vrow + 4 * j);
+      const f32x4 g4 = *reinterpret_cast<const f32x4*>(&gl[w][col][h * DH + 4 * j]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dp = __builtin_amdgcn_mfma_f32_32x32x2f32(v4[e], g4[e], dp, 0, 0, 0);
+    }
+    // dS^T of key n0 + 8(r/4) + 4h + (r mod 4), query qrow
+    float ds[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kj = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      float x = s[r] * zc - l2[0];
+      if (bias == BIAS_ALIBI) x -= slope * (float)abs(qrow - kj);
+      const bool vis = kj < p.Nkv && f32_visible(mask, p.window, qrow, kj);
+      const float pr = vis ? __builtin_amdgcn_exp2f(x) : 0.f;
+      ds[r] = pr * (dp[r] - l2[1]);
+    }
+    // dQ^T += k~^T dS^T
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kj = min(n0 + 8 * (i >> 2) + 4 * h + (i & 3), p.Nkv - 1);
+      const VecC kv = *reinterpret_cast<const VecC*>(kt + (int64_t)kj * p.kts[2] + DC * col);
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        float kc;
+        if constexpr (DC == 1) kc = kv;
+        else kc = kv[c];
+        dq[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(kc, ds[i], dq[c], 0, 0, 0);
+      }
+    }
+  }
+
+  if (qrow >= p.Nq) return;
+#pragma unroll
+  for (int c = 0; c < DC; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[c][r] *= p.scale;
+  if (rope) {
+    // d = DC (8(r/4) + 4h + (r mod 4)) + c: registers r < 8 hold d < D/2,
+    // and register r + 8 holds the partner d + D/2
+    const float* cr = reinterpret_cast<const float*>(p.cos) + (int64_t)qrow * p.rs[0];
+    const float* sr = reinterpret_cast<const float*>(p.sin) + (int64_t)qrow * p.rs[0];
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        const int d = DC * (8 * (r >> 2) + 4 * h + (r & 3)) + c;
+        float l = dq[c][r], hh = dq[c][r + 8];
+        f32_rope_back(l, hh, cr[d], sr[d], cr[d + DH], sr[d + DH]);
+        dq[c][r] = l;
+        dq[c][r + 8] = hh;
+      }
+  }
+  float* dqr = reinterpret_cast<float*>(p.dq) + b * p.dqs[0] + hq * p.dqs[1] + (int64_t)qrow * p.dqs[2];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int d0 = DC * (8 * (r >> 2) + 4 * h + (r & 3));
+    VecC st;
+    if constexpr (DC == 1) {
+      st = dq[0][r];
+    } else {
+#pragma unroll
+      for (int c = 0; c < DC; ++c) st[c] = dq[c][r];
+    }
+    *reinterpret_cast<VecC*>(dqr + d0) = st;
+  }
+}
+
+}  // namespace af

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "attnfuse_hip.h"
 #include "fwd_kernel.hpp"
 #include "rope_kernel.hpp"
 
@@ -41,6 +42,8 @@ AF_DECLARE_ROPE(launch_rope_bf16_d128)
 // a head dim with no instantiation.
 struct FwdF32Params;
 int launch_fwd_f32(const FwdF32Params& p, int head_dim, dim3 grid, hipStream_t s);
+struct BwdParams;
+int launch_bwd_f32(BwdParams p, const af_bwd_args& a, hipStream_t s);
 int launch_rope_f32(const float* x, float* out, const float* cs, const float* sn, const int64_t* xs, int64_t rs,
                     int H, int N, int64_t rows, int head_dim, hipStream_t s);
 

@@ -78,8 +78,8 @@ def test_query_and_tile():
 
 
 def test_fp32_outside_the_forward_is_rejected():
-    """fp32 has a forward kernel only: the backward, decode and block-sparse
-    entry points reject it with an error that names the dtypes they take."""
+    """fp32 has forward and backward kernels but no decode or block-sparse
+    ones: those entry points reject it with an error naming fp16/bf16."""
     lib = N.lib()
     a = N.DecodeArgsC()
     a.key = N.SpecKeyC(2, 64, 0, 0, 0, 0)
