@@ -30,6 +30,7 @@ HBM, every step exactly one kernel launch.  The same line carries
   mask fixture): 14*B*H*D*4096*n_active FLOP per fwd+bwd step;
 * ``train`` -- config 5 (causal GQA + fused RoPE base 5e5, fwd+bwd, bf16,
   B=1 N=4096 H_q=32 H_kv=8 D=128): 3.5 x 4*B*H_q*D*N(N+1)/2 FLOP per step;
+* ``train_fp32`` -- config 5 on fp32 inputs, against the fp32 MFMA peak;
 * ``cpu_baseline`` -- the fp32 CPU oracle (a restatement of the reference's
   naive attention) on a bounded sample of config 2's heads, on the host's
   cores, plus config 1 (GPT-2-small causal, B=1 H=12 N=512 D=64, fp32) in
@@ -234,7 +235,7 @@ def bench_bigbird(steps, warmup):
             "algorithmic_flop_per_step": flops}
 
 
-def bench_train(steps, warmup):
+def bench_train(steps, warmup, dtype=None):
     """Config 5: causal GQA + fused RoPE (base 5e5) forward + backward."""
     import torch
 
@@ -244,13 +245,14 @@ def bench_train(steps, warmup):
     from attentionfuse_amd.runtime.prepared import prepare_attention
 
     dev = torch.device("cuda:0")
+    dtype = torch.bfloat16 if dtype is None else dtype
     B, Hq, Hkv, N, D = C5["B"], C5["Hq"], C5["Hkv"], C5["N"], C5["D"]
     g = torch.Generator(device=dev).manual_seed(0)
-    Q = torch.randn(B, Hq, N, D, generator=g, device=dev, dtype=torch.bfloat16)
-    K = torch.randn(B, Hkv, N, D, generator=g, device=dev, dtype=torch.bfloat16)
-    V = torch.randn(B, Hkv, N, D, generator=g, device=dev, dtype=torch.bfloat16)
-    dO = torch.randn(B, Hq, N, D, generator=g, device=dev, dtype=torch.bfloat16)
-    cos, sin = build_rope_cache(N, D, base=500000.0, device=dev, dtype=torch.bfloat16)
+    Q = torch.randn(B, Hq, N, D, generator=g, device=dev, dtype=dtype)
+    K = torch.randn(B, Hkv, N, D, generator=g, device=dev, dtype=dtype)
+    V = torch.randn(B, Hkv, N, D, generator=g, device=dev, dtype=dtype)
+    dO = torch.randn(B, Hq, N, D, generator=g, device=dev, dtype=dtype)
+    cos, sin = build_rope_cache(N, D, base=500000.0, device=dev, dtype=dtype)
     fn = af.attention(lambda Q, K, V: af.softmax(af.causal(af.rope(Q, K))) @ V)
     graph = fn(Q, K, V, return_graph=True)
     L = torch.empty(B, Hq, N, dtype=torch.float32, device=dev)
@@ -262,10 +264,12 @@ def bench_train(steps, warmup):
         run_backward(graph, Q, K, V, out, L, dO, scale, cos=cos, sin=sin)
     ms = _time_launch(step, steps, warmup)
     flops = int(3.5 * causal_flops(B, Hq, N, D))
-    return {"workload": "config 5: causal GQA + RoPE(base 5e5) fwd+bwd bf16 "
-                        "B=1 N=4096 Hq=32 Hkv=8 D=128",
+    f32 = dtype == torch.float32
+    peak = PEAK_FP32_TFLOPS if f32 else PEAK_FP16_TFLOPS
+    return {"workload": "config 5: causal GQA + RoPE(base 5e5) fwd+bwd %s "
+                        "B=1 N=4096 Hq=32 Hkv=8 D=128" % ("fp32" if f32 else "bf16"),
             "ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
-            "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+            "frac": round(flops / (ms * 1e-3) / 1e12 / peak, 4),
             "algorithmic_flop_per_step": flops}
 
 
@@ -444,6 +448,9 @@ def main():
     if not args.no_train:
         line["bigbird"] = bench_bigbird(max(args.steps // 2, 1), max(args.warmup // 2, 1))
         line["train"] = bench_train(max(args.steps // 2, 1), max(args.warmup // 2, 1))
+        if not args.no_fp32:
+            import torch
+            line["train_fp32"] = bench_train(max(args.steps // 5, 1), 1, dtype=torch.float32)
     if not args.no_cpu:
         cb, err = cpu_baseline(tensors)
         line["cpu_baseline"] = cb

@@ -66,7 +66,7 @@ typedef enum af_norm { AF_NORM_SOFTMAX = 0, AF_NORM_RELU = 1 } af_norm;
 /* Specialisation key: replaces the reference's Triton constexpr record
  * (attnfuse/compiler/codegen.py:391-404; attnfuse/ir/tiled.py:52-81). */
 typedef struct af_spec_key {
-  int32_t dtype;     /* af_dtype; AF_F32: af_fwd only (not block-sparse) */
+  int32_t dtype;     /* af_dtype; AF_F32: af_fwd and af_bwd, not block-sparse or decode */
   int32_t head_dim;  /* instantiated: 32, 64, 128 (af_query) */
   int32_t mask;      /* af_mask                   */
   int32_t bias;      /* af_bias                   */
@@ -190,6 +190,8 @@ typedef struct af_bwd_args {
  * (grids of at most two workgroups per CU), fp32 dK and dV partial sums
  * per split. */
 size_t af_bwd_workspace_bytes(const af_bwd_args* args);
+/* fp16 / bf16, or AF_F32 (fp32 throughout on the fp32 MFMAs; dense, causal
+ * and windowed masks only, bm must then be NULL). */
 int af_bwd(const af_bwd_args* args, const af_blockmask* bm /* nullable */,
            void* workspace, size_t workspace_bytes, void* stream);
 
