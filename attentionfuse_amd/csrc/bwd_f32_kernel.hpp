@@ -8,9 +8,10 @@
 //
 //   bwd_prep_f32_kernel  per query row: delta = sum_d dO O and L log2(e)
 //                        (0 for a row that sees no key) into the workspace.
-//   bwd_dkv_f32_kernel   a wave owns 32 keys; its k~ and v rows sit in LDS.
-//                        For every query head of its group and 32-row query
-//                        tile: S = q~ k~^T and dP = dO v^T with queries as
+//   bwd_dkv_f32_kernel   a wave owns 32 keys.  For every query head of its
+//                        group and 32-row query tile, staged once in LDS for
+//                        the workgroup's four waves: S = q~ k~^T and
+//                        dP = dO v^T with queries as
 //                        the MFMA rows, P and dS from the saved L and delta,
 //                        dV += P^T dO, dK += dS^T q~.  Register r of lane l
 //                        holds query 8(r/4) + 4h + (r mod 4) of key l mod 32
@@ -78,49 +79,43 @@ __device__ __forceinline__ void f32_rope_back(float& lo, float& hi, float clo, f
 template <int D>
 __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const BwdParams p, int mask, int bias,
                                                                          int rope) {
-  constexpr int DH = D / 2, DC = D / 32, KP = D + 4;
+  constexpr int DH = D / 2, DC = D / 32, QP = D + 4;
   typedef typename F32Vec<DC>::T VecC;
-  __shared__ __attribute__((aligned(16))) float kl[kBwdF32Waves][32][KP];
-  __shared__ __attribute__((aligned(16))) float vl[kBwdF32Waves][32][KP];
+  // the current query tile's q~ and dO rows, shared by the four waves
+  __shared__ __attribute__((aligned(16))) float ql[32][QP];
+  __shared__ __attribute__((aligned(16))) float gl[32][QP];
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int col = lane & 31, h = lane >> 5;
   const int nbh = p.B * p.Hkv;
   const int kb = (int)(blockIdx.x / nbh), bh = (int)(blockIdx.x % nbh);
   const int b = bh / p.Hkv, hk = bh % p.Hkv;
-  const int k0 = kb * kBwdF32Block + w * 32;
+  const int kw0 = kb * kBwdF32Block;  // first key of the workgroup
+  const int k0 = kw0 + w * 32;
 
-  const float* kt = reinterpret_cast<const float*>(p.kt) + b * p.kts[0] + hk * p.kts[1];
-  const float* vg = reinterpret_cast<const float*>(p.v) + b * p.vs[0] + hk * p.vs[1];
-  for (int idx = lane; idx < 32 * (D / 4); idx += 64) {
-    const int r = idx / (D / 4), c4 = (idx % (D / 4)) * 4;
-    const int n = k0 + r;
-    f32x4 kv4 = {0.f, 0.f, 0.f, 0.f}, vv4 = {0.f, 0.f, 0.f, 0.f};
-    if (n < p.Nkv) {
-      kv4 = *reinterpret_cast<const f32x4*>(kt + (int64_t)n * p.kts[2] + c4);
-      vv4 = *reinterpret_cast<const f32x4*>(vg + (int64_t)n * p.vs[2] + c4);
-    }
-    *reinterpret_cast<f32x4*>(&kl[w][r][c4]) = kv4;
-    *reinterpret_cast<f32x4*>(&vl[w][r][c4]) = vv4;
-  }
-  __syncthreads();
-  if (k0 >= p.Nkv) return;
-
-  // query tiles that can see one of keys [k0, k0 + 32)
+  // Query tiles that can see a key of the workgroup: one range for all four
+  // waves (set by the workgroup index only), so every wave runs the same
+  // loop and reaches every barrier; a wave whose keys start past N_kv
+  // computes masked tiles and stores nothing.
   int q_lo = 0, q_hi = p.Nq;
   if (mask == MASK_CAUSAL) {
-    q_lo = k0;
+    q_lo = kw0;
   } else if (mask == MASK_SW) {
-    q_lo = max(0, k0 - p.window + 1);
-    q_hi = min(q_hi, k0 + 31 + p.window);
+    q_lo = max(0, kw0 - p.window + 1);
+    q_hi = min(q_hi, kw0 + kBwdF32Block - 1 + p.window);
   } else if (mask == MASK_CSW) {
-    q_lo = k0;
-    q_hi = min(q_hi, k0 + 31 + p.window);
+    q_lo = kw0;
+    q_hi = min(q_hi, kw0 + kBwdF32Block - 1 + p.window);
   }
   q_lo &= ~31;
 
   const float zc = p.scale * kLog2e;
   const int key = k0 + col;  // this lane's key in S and dP
+  // k~ and v half rows of this lane's key (clamped; keys >= N_kv are masked)
+  const float* krow = reinterpret_cast<const float*>(p.kt) + b * p.kts[0] + hk * p.kts[1] +
+                      (int64_t)min(key, p.Nkv - 1) * p.kts[2] + h * DH;
+  const float* vrow = reinterpret_cast<const float*>(p.v) + b * p.vs[0] + hk * p.vs[1] +
+                      (int64_t)min(key, p.Nkv - 1) * p.vs[2] + h * DH;
   f32x16 dk[DC], dv[DC];
 #pragma unroll
   for (int c = 0; c < DC; ++c)
@@ -134,24 +129,34 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const Bw
     const float* dog = reinterpret_cast<const float*>(p.dout) + b * p.dos[0] + hq * p.dos[1];
     const float* ld = p.ld + 2 * ((int64_t)(b * p.Hq + hq) * p.Nq);
     for (int q0 = q_lo; q0 < q_hi; q0 += 32) {
+      __syncthreads();  // every wave is done with the previous tile
+      for (int idx = threadIdx.x; idx < 32 * (D / 4); idx += kBwdF32Waves * 64) {
+        const int r = idx / (D / 4), c4 = (idx % (D / 4)) * 4;
+        const int n = q0 + r;
+        f32x4 a = {0.f, 0.f, 0.f, 0.f}, g = {0.f, 0.f, 0.f, 0.f};
+        if (n < p.Nq) {
+          a = *reinterpret_cast<const f32x4*>(qt + (int64_t)n * p.qts[2] + c4);
+          g = *reinterpret_cast<const f32x4*>(dog + (int64_t)n * p.dos[2] + c4);
+        }
+        *reinterpret_cast<f32x4*>(&ql[r][c4]) = a;
+        *reinterpret_cast<f32x4*>(&gl[r][c4]) = g;
+      }
+      __syncthreads();
       // S and dP: queries q0 + (l mod 32) as the A rows, d paired across halves
-      const int qa = min(q0 + col, p.Nq - 1);
-      const float* qrow = qt + (int64_t)qa * p.qts[2] + h * DH;
-      const float* grow = dog + (int64_t)qa * p.dos[2] + h * DH;
       f32x16 s, dp;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
 #pragma unroll
       for (int j = 0; j < DH / 4; ++j) {
-        const f32x4 qa4 = *reinterpret_cast<const f32x4*>(qrow + 4 * j);
-        const f32x4 ka4 = *reinterpret_cast<const f32x4*>(&kl[w][col][h * DH + 4 * j]);
+        const f32x4 qa4 = *reinterpret_cast<const f32x4*>(&ql[col][h * DH + 4 * j]);
+        const f32x4 ka4 = *reinterpret_cast<const f32x4*>(krow + 4 * j);
 #pragma unroll
         for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(qa4[e], ka4[e], s, 0, 0, 0);
       }
 #pragma unroll
       for (int j = 0; j < DH / 4; ++j) {
-        const f32x4 ga4 = *reinterpret_cast<const f32x4*>(grow + 4 * j);
-        const f32x4 va4 = *reinterpret_cast<const f32x4*>(&vl[w][col][h * DH + 4 * j]);
+        const f32x4 ga4 = *reinterpret_cast<const f32x4*>(&gl[col][h * DH + 4 * j]);
+        const f32x4 va4 = *reinterpret_cast<const f32x4*>(vrow + 4 * j);
 #pragma unroll
         for (int e = 0; e < 4; ++e) dp = __builtin_amdgcn_mfma_f32_32x32x2f32(ga4[e], va4[e], dp, 0, 0, 0);
       }
@@ -167,13 +172,13 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const Bw
         pr[r] = vis ? __builtin_amdgcn_exp2f(x) : 0.f;
         ds[r] = pr[r] * (dp[r] - l2[1]);
       }
-      // dV += P^T dO and dK += dS^T q~: B operands are rows of dO / q~ at the
+      // dV += P^T dO and dK += dS^T q~: B operands are the LDS rows of the
       // queries of register i, D/32 consecutive d per lane
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int qi = min(q0 + 8 * (i >> 2) + 4 * h + (i & 3), p.Nq - 1);
-        const VecC gv = *reinterpret_cast<const VecC*>(dog + (int64_t)qi * p.dos[2] + DC * col);
-        const VecC qv = *reinterpret_cast<const VecC*>(qt + (int64_t)qi * p.qts[2] + DC * col);
+        const int qi = 8 * (i >> 2) + 4 * h + (i & 3);
+        const VecC gv = *reinterpret_cast<const VecC*>(&gl[qi][DC * col]);
+        const VecC qv = *reinterpret_cast<const VecC*>(&ql[qi][DC * col]);
 #pragma unroll
         for (int c = 0; c < DC; ++c) {
           float gc, qc;
@@ -190,6 +195,7 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const Bw
       }
     }
   }
+  if (k0 >= p.Nkv) return;
 
   // dK (scaled, rotated back with RoPE) and dV rows k0 + 8(r/4) + 4h + (r mod 4)
 #pragma unroll
