@@ -17,9 +17,10 @@
 //                        holds query 8(r/4) + 4h + (r mod 4) of key l mod 32
 //                        (h = l / 32), which is the query the A operand of
 //                        the r-th dV / dK MFMA needs from that lane.
-//   bwd_dq_f32_kernel    a wave owns 32 queries; its q~ and dO rows sit in
-//                        LDS.  Per 32-key tile: S^T and dP^T with keys as
-//                        the MFMA rows, dS^T, dQ^T += k~^T dS^T.
+//   bwd_dq_f32_kernel    a wave owns 32 queries; its q~ and dO half rows sit
+//                        in registers.  Per 32-key tile, staged once in LDS
+//                        for the workgroup's four waves: S^T and dP^T with
+//                        keys as the MFMA rows, dS^T, dQ^T += k~^T dS^T.
 //
 // Output block c, row m of dV, dK and dQ^T holds d = (D/32) m + c, so a
 // lane's operand reads and stores are D/32 consecutive floats.  With RoPE
@@ -246,10 +247,11 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const Bw
 template <int D>
 __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dq_f32_kernel(const BwdParams p, int mask, int bias,
                                                                         int rope) {
-  constexpr int DH = D / 2, DC = D / 32, QP = D + 4;
+  constexpr int DH = D / 2, DC = D / 32, KP = D + 4;
   typedef typename F32Vec<DC>::T VecC;
-  __shared__ __attribute__((aligned(16))) float ql[kBwdF32Waves][32][QP];
-  __shared__ __attribute__((aligned(16))) float gl[kBwdF32Waves][32][QP];
+  // the current key tile's k~ and v rows, shared by the four waves
+  __shared__ __attribute__((aligned(16))) float kl[32][KP];
+  __shared__ __attribute__((aligned(16))) float vl[32][KP];
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int col = lane & 31, h = lane >> 5;
@@ -258,40 +260,39 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dq_f32_kernel(const Bwd
   const int bh = (int)(blockIdx.x % nbh);
   if (mask == MASK_CAUSAL || mask == MASK_CSW) mb = p.n_qblocks - 1 - mb;
   const int b = bh / p.Hq, hq = bh % p.Hq, hk = hq / p.G;
-  const int q0 = mb * kBwdF32Block + w * 32;
+  const int qw0 = mb * kBwdF32Block;  // first query of the workgroup
+  const int q0 = qw0 + w * 32;
   const int qrow = q0 + col;
+  const int qc = min(qrow, p.Nq - 1);  // clamped: rows >= N_q compute, store nothing
 
-  const float* qt = reinterpret_cast<const float*>(p.qt) + b * p.qts[0] + hq * p.qts[1];
-  const float* dog = reinterpret_cast<const float*>(p.dout) + b * p.dos[0] + hq * p.dos[1];
-  for (int idx = lane; idx < 32 * (D / 4); idx += 64) {
-    const int r = idx / (D / 4), c4 = (idx % (D / 4)) * 4;
-    const int n = q0 + r;
-    f32x4 a = {0.f, 0.f, 0.f, 0.f}, g = {0.f, 0.f, 0.f, 0.f};
-    if (n < p.Nq) {
-      a = *reinterpret_cast<const f32x4*>(qt + (int64_t)n * p.qts[2] + c4);
-      g = *reinterpret_cast<const f32x4*>(dog + (int64_t)n * p.dos[2] + c4);
-    }
-    *reinterpret_cast<f32x4*>(&ql[w][r][c4]) = a;
-    *reinterpret_cast<f32x4*>(&gl[w][r][c4]) = g;
+  // this lane's q~ and dO half rows: the B operands of S^T and dP^T
+  const float* qt = reinterpret_cast<const float*>(p.qt) + b * p.qts[0] + hq * p.qts[1] + (int64_t)qc * p.qts[2];
+  const float* dog = reinterpret_cast<const float*>(p.dout) + b * p.dos[0] + hq * p.dos[1] + (int64_t)qc * p.dos[2];
+  f32x4 qh[DH / 4], gh[DH / 4];
+#pragma unroll
+  for (int j = 0; j < DH / 4; ++j) {
+    qh[j] = *reinterpret_cast<const f32x4*>(qt + h * DH + 4 * j);
+    gh[j] = *reinterpret_cast<const f32x4*>(dog + h * DH + 4 * j);
   }
-  __syncthreads();
-  if (q0 >= p.Nq) return;
 
+  // Key tiles one of the workgroup's queries can see: one range for all four
+  // waves (set by the workgroup index only), so every wave runs the same
+  // loop and reaches every barrier.
   int n_lo = 0, n_hi = p.Nkv;
   if (mask == MASK_CAUSAL) {
-    n_hi = min(n_hi, q0 + 32);
+    n_hi = min(n_hi, qw0 + kBwdF32Block);
   } else if (mask == MASK_SW) {
-    n_lo = max(0, q0 - p.window + 1);
-    n_hi = min(n_hi, q0 + 31 + p.window);
+    n_lo = max(0, qw0 - p.window + 1);
+    n_hi = min(n_hi, qw0 + kBwdF32Block - 1 + p.window);
   } else if (mask == MASK_CSW) {
-    n_lo = max(0, q0 - p.window + 1);
-    n_hi = min(n_hi, q0 + 32);
+    n_lo = max(0, qw0 - p.window + 1);
+    n_hi = min(n_hi, qw0 + kBwdF32Block);
   }
   n_lo &= ~31;
 
   const float zc = p.scale * kLog2e;
   const float slope = bias == BIAS_ALIBI ? p.slopes[hq] * kLog2e : 0.f;
-  const f32x2 l2 = *reinterpret_cast<const f32x2*>(p.ld + 2 * ((int64_t)(b * p.Hq + hq) * p.Nq + min(qrow, p.Nq - 1)));
+  const f32x2 l2 = *reinterpret_cast<const f32x2*>(p.ld + 2 * ((int64_t)(b * p.Hq + hq) * p.Nq + qc));
   const float* kt = reinterpret_cast<const float*>(p.kt) + b * p.kts[0] + hk * p.kts[1];
   const float* vg = reinterpret_cast<const float*>(p.v) + b * p.vs[0] + hk * p.vs[1];
 
@@ -302,25 +303,33 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dq_f32_kernel(const Bwd
     for (int r = 0; r < 16; ++r) dq[c][r] = 0.f;
 
   for (int n0 = n_lo; n0 < n_hi; n0 += 32) {
-    const int ka = min(n0 + col, p.Nkv - 1);
-    const float* krow = kt + (int64_t)ka * p.kts[2] + h * DH;
-    const float* vrow = vg + (int64_t)ka * p.vs[2] + h * DH;
+    __syncthreads();  // every wave is done with the previous tile
+    for (int idx = threadIdx.x; idx < 32 * (D / 4); idx += kBwdF32Waves * 64) {
+      const int r = idx / (D / 4), c4 = (idx % (D / 4)) * 4;
+      const int n = n0 + r;
+      f32x4 a = {0.f, 0.f, 0.f, 0.f}, v = {0.f, 0.f, 0.f, 0.f};
+      if (n < p.Nkv) {
+        a = *reinterpret_cast<const f32x4*>(kt + (int64_t)n * p.kts[2] + c4);
+        v = *reinterpret_cast<const f32x4*>(vg + (int64_t)n * p.vs[2] + c4);
+      }
+      *reinterpret_cast<f32x4*>(&kl[r][c4]) = a;
+      *reinterpret_cast<f32x4*>(&vl[r][c4]) = v;
+    }
+    __syncthreads();
     f32x16 s, dp;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
 #pragma unroll
     for (int j = 0; j < DH / 4; ++j) {
-      const f32x4 k4 = *reinterpret_cast<const f32x4*>(krow + 4 * j);
-      const f32x4 q4 = *reinterpret_cast<const f32x4*>(&ql[w][col][h * DH + 4 * j]);
+      const f32x4 k4 = *reinterpret_cast<const f32x4*>(&kl[col][h * DH + 4 * j]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(k4[e], q4[e], s, 0, 0, 0);
+      for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(k4[e], qh[j][e], s, 0, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < DH / 4; ++j) {
-      const f32x4 v4 = *reinterpret_cast<const f32x4*>(vrow + 4 * j);
-      const f32x4 g4 = *reinterpret_cast<const f32x4*>(&gl[w][col][h * DH + 4 * j]);
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(&vl[col][h * DH + 4 * j]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) dp = __builtin_amdgcn_mfma_f32_32x32x2f32(v4[e], g4[e], dp, 0, 0, 0);
+      for (int e = 0; e < 4; ++e) dp = __builtin_amdgcn_mfma_f32_32x32x2f32(v4[e], gh[j][e], dp, 0, 0, 0);
     }
     // dS^T of key n0 + 8(r/4) + 4h + (r mod 4), query qrow
     float ds[16];
@@ -329,15 +338,15 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dq_f32_kernel(const Bwd
       const int kj = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
       float x = s[r] * zc - l2[0];
       if (bias == BIAS_ALIBI) x -= slope * (float)abs(qrow - kj);
-      const bool vis = kj < p.Nkv && f32_visible(mask, p.window, qrow, kj);
+      const bool vis = qrow < p.Nq && kj < p.Nkv && f32_visible(mask, p.window, qrow, kj);
       const float pr = vis ? __builtin_amdgcn_exp2f(x) : 0.f;
       ds[r] = pr * (dp[r] - l2[1]);
     }
-    // dQ^T += k~^T dS^T
+    // dQ^T += k~^T dS^T, k~ rows of the keys of register i from LDS
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int kj = min(n0 + 8 * (i >> 2) + 4 * h + (i & 3), p.Nkv - 1);
-      const VecC kv = *reinterpret_cast<const VecC*>(kt + (int64_t)kj * p.kts[2] + DC * col);
+      const int kj = 8 * (i >> 2) + 4 * h + (i & 3);
+      const VecC kv = *reinterpret_cast<const VecC*>(&kl[kj][DC * col]);
 #pragma unroll
       for (int c = 0; c < DC; ++c) {
         float kc;
