@@ -19,6 +19,18 @@ int bwd_group_split(const af_bwd_args& a) {
   return gs;
 }
 
+// fp32 dK/dV: split the group's query heads until the grid holds about four
+// 4-wave workgroups per CU (256 CUs); causal key blocks differ in work by up
+// to N/128 times, so one workgroup per key block leaves most CUs idle at the end.
+int bwd_group_split_f32(const af_bwd_args& a) {
+  if (a.batch <= 0 || a.heads_kv <= 0 || a.heads_q <= 0 || a.seqlen_kv <= 0 || a.heads_q % a.heads_kv != 0) return 1;
+  const int G = a.heads_q / a.heads_kv;
+  const int64_t base = (int64_t)((a.seqlen_kv + 127) / 128) * a.batch * a.heads_kv;
+  int gs = 1;
+  while (G % (2 * gs) == 0 && base * 2 * gs <= 1024) gs *= 2;
+  return gs;
+}
+
 BwdWorkspace bwd_workspace_layout(const af_bwd_args& a) {
   auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
   BwdWorkspace w{0, 0, 0, 0, 0, 0, 1};
@@ -35,8 +47,7 @@ BwdWorkspace bwd_workspace_layout(const af_bwd_args& a) {
     w.kr = w.total;
     w.total += up(rows_k * a.key.head_dim * elem);
   }
-  // the fp32 dK/dV kernel sums its whole GQA group itself
-  w.g_split = a.key.dtype == AF_F32 ? 1 : bwd_group_split(a);
+  w.g_split = a.key.dtype == AF_F32 ? bwd_group_split_f32(a) : bwd_group_split(a);
   if (w.g_split > 1) {
     w.dkp = w.total;
     w.total += up((size_t)w.g_split * rows_k * a.key.head_dim * 4);

@@ -11,9 +11,15 @@ static void launch_bwd_f32_d(BwdParams p, int mask, int bias, int rope, hipStrea
   const int64_t rows_q = (int64_t)p.B * p.Hq * p.Nq;
   if (rows_q > 0)
     hipLaunchKernelGGL((bwd_prep_f32_kernel<D>), dim3((unsigned)((rows_q + 255) / 256)), dim3(256), 0, s, p);
-  const unsigned grid_kv = (unsigned)(p.n_kblocks * p.B * p.Hkv);
-  if (grid_kv > 0)
+  const unsigned grid_kv = (unsigned)(p.n_kblocks * p.g_split * p.B * p.Hkv);
+  if (grid_kv > 0) {
     hipLaunchKernelGGL((bwd_dkv_f32_kernel<D>), dim3(grid_kv), dim3(kBwdF32Waves * 64), 0, s, p, mask, bias, rope);
+    if (p.g_split > 1) {
+      const int64_t threads = (int64_t)p.B * p.Hkv * p.Nkv * (D / 4);
+      hipLaunchKernelGGL((bwd_dkv_combine_f32_kernel<D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                         p);
+    }
+  }
   const unsigned grid_q = (unsigned)(p.n_qblocks * p.B * p.Hq);
   if (grid_q > 0)
     hipLaunchKernelGGL((bwd_dq_f32_kernel<D>), dim3(grid_q), dim3(kBwdF32Waves * 64), 0, s, p, mask, bias, rope);

@@ -88,10 +88,15 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const Bw
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int col = lane & 31, h = lane >> 5;
+  // workgroup = (key block, group split, b, h_kv), key block slowest; split
+  // gsi takes query heads [gsi G/g_split, (gsi + 1) G/g_split) of the group
   const int nbh = p.B * p.Hkv;
-  const int kb = (int)(blockIdx.x / nbh), bh = (int)(blockIdx.x % nbh);
+  const int kb = (int)(blockIdx.x / (nbh * p.g_split));
+  const int gsi = (int)(blockIdx.x / nbh) % p.g_split;
+  const int bh = (int)(blockIdx.x % nbh);
   const int b = bh / p.Hkv, hk = bh % p.Hkv;
   const int kw0 = kb * kBwdF32Block;  // first key of the workgroup
+  const int gpw = p.G / p.g_split;
   const int k0 = kw0 + w * 32;
 
   // Query tiles that can see a key of the workgroup: one range for all four
@@ -123,7 +128,7 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const Bw
 #pragma unroll
     for (int r = 0; r < 16; ++r) dk[c][r] = dv[c][r] = 0.f;
 
-  for (int gi = 0; gi < p.G; ++gi) {
+  for (int gi = gsi * gpw; gi < (gsi + 1) * gpw; ++gi) {
     const int hq = hk * p.G + gi;
     const float slope = bias == BIAS_ALIBI ? p.slopes[hq] * kLog2e : 0.f;
     const float* qt = reinterpret_cast<const float*>(p.qt) + b * p.qts[0] + hq * p.qts[1];
@@ -222,8 +227,17 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const Bw
       }
     }
   }
+  // one split: final dK / dV; several: this split's partial sums (already
+  // scaled and rotated back, both linear) in (g_split, B, Hkv, Nkv, D)
   float* dkg = reinterpret_cast<float*>(p.dk) + b * p.dks[0] + hk * p.dks[1];
   float* dvg = reinterpret_cast<float*>(p.dv) + b * p.dvs[0] + hk * p.dvs[1];
+  int64_t dks2 = p.dks[2], dvs2 = p.dvs[2];
+  if (p.g_split > 1) {
+    const int64_t off = (((int64_t)gsi * p.B + b) * p.Hkv + hk) * p.Nkv * D;
+    dkg = p.dkp + off;
+    dvg = p.dvp + off;
+    dks2 = dvs2 = D;
+  }
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int kr = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -239,9 +253,34 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const Bw
         v[c] = dv[c][r];
       }
     }
-    *reinterpret_cast<VecC*>(dkg + (int64_t)kr * p.dks[2] + DC * col) = a;
-    *reinterpret_cast<VecC*>(dvg + (int64_t)kr * p.dvs[2] + DC * col) = v;
+    *reinterpret_cast<VecC*>(dkg + (int64_t)kr * dks2 + DC * col) = a;
+    *reinterpret_cast<VecC*>(dvg + (int64_t)kr * dvs2 + DC * col) = v;
   }
+}
+
+// dK, dV row = the sum of the g_split partial rows, in split order (the
+// result does not depend on which workgroup finished first).  One thread per
+// (row r = (b Hkv + h) Nkv + n, 4 consecutive d).
+template <int D>
+__global__ void __launch_bounds__(256) bwd_dkv_combine_f32_kernel(const BwdParams p) {
+  const int64_t rows = (int64_t)p.B * p.Hkv * p.Nkv;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t r = t / (D / 4);
+  if (r >= rows) return;
+  const int d = (int)(t % (D / 4)) * 4;
+  const int n = (int)(r % p.Nkv);
+  const int64_t bh = r / p.Nkv;
+  const int hk = (int)(bh % p.Hkv), b = (int)(bh / p.Hkv);
+  f32x4 sk = *reinterpret_cast<const f32x4*>(p.dkp + r * D + d);
+  f32x4 sv = *reinterpret_cast<const f32x4*>(p.dvp + r * D + d);
+  for (int sp = 1; sp < p.g_split; ++sp) {
+    sk += *reinterpret_cast<const f32x4*>(p.dkp + (sp * rows + r) * D + d);
+    sv += *reinterpret_cast<const f32x4*>(p.dvp + (sp * rows + r) * D + d);
+  }
+  *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.dk) + b * p.dks[0] + hk * p.dks[1] + (int64_t)n * p.dks[2] +
+                            d) = sk;
+  *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.dv) + b * p.dvs[0] + hk * p.dvs[1] + (int64_t)n * p.dvs[2] +
+                            d) = sv;
 }
 
 template <int D>
