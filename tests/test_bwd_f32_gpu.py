@@ -92,3 +92,20 @@ def test_backward_with_an_empty_side(Nq, Nkv):
     for t in (q, k, v):
         assert t.grad is not None and t.grad.shape == t.shape
         assert torch.count_nonzero(t.grad) == 0
+
+
+def test_backward_deterministic():
+    """The GQA group is split over workgroups whose partial sums are added in
+    split order: two runs give bit-identical gradients."""
+    g = torch.Generator(device="cuda").manual_seed(11)
+    Q = torch.randn(1, 8, 384, 64, generator=g, device="cuda", dtype=F32)
+    K, V = (torch.randn(1, 2, 384, 64, generator=g, device="cuda", dtype=F32) for _ in range(2))
+    dO = torch.randn(1, 8, 384, 64, generator=g, device="cuda", dtype=F32)
+    grads = []
+    for _ in range(2):
+        q, k, v = (t.clone().requires_grad_(True) for t in (Q, K, V))
+        _fn("causal", 8)(q, k, v).backward(dO)
+        grads.append((q.grad, k.grad, v.grad))
+    torch.cuda.synchronize()
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
