@@ -255,6 +255,88 @@ int dispatch_fwd_f32(const af_fwd_args& a, void* workspace, size_t workspace_byt
 }
 
 }  // namespace
+
+// Validation and launch geometry of a decode call (af_decode and
+// af_decode_noalloc): fills every field of *p except the workspace
+// pointers and sets *need to the workspace bytes of the split count used.
+// max_ws > 0 bounds the workspace: a library-chosen split count is lowered
+// until the partials fit, and an explicit one that does not fit is refused.
+int plan_decode(const af_decode_args* a, size_t max_ws, DecodeParams* out, size_t* need) {
+  if (a == nullptr) return fail(AF_ERR_BAD_ARG, "args is NULL");
+  int rc;
+  if ((rc = check_bhnd("q", a->q, a->q_stride, 1))) return rc;
+  if ((rc = check_bhnd("k", a->k, a->k_stride, a->seqlen_kv))) return rc;
+  if ((rc = check_bhnd("v", a->v, a->v_stride, a->seqlen_kv))) return rc;
+  if (a->o == nullptr) return fail(AF_ERR_BAD_ARG, "o is NULL");
+  if (a->o_stride[3] != 1) return fail(AF_ERR_BAD_ARG, "o: head-dim stride must be 1");
+  if ((rc = check_key(a->key, false))) return rc;
+  if (a->key.mask != AF_MASK_FULL || a->key.rope != 0 || a->key.norm != AF_NORM_SOFTMAX ||
+      (a->key.bias != AF_BIAS_NONE && a->key.bias != AF_BIAS_ALIBI))
+    return fail(AF_ERR_UNSUPPORTED, "decode takes dense softmax with no bias or ALiBi, no RoPE");
+  if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seqlen_kv <= 0 ||
+      a->heads_q % a->heads_kv != 0)
+    return fail(AF_ERR_BAD_ARG, "bad decode sizes B=%d Hq=%d Hkv=%d Nkv=%d", a->batch, a->heads_q, a->heads_kv,
+                a->seqlen_kv);
+  if (a->key.bias == AF_BIAS_ALIBI && a->alibi_slopes == nullptr) return fail(AF_ERR_BAD_ARG, "ALiBi needs slopes");
+  const int D = a->key.head_dim;
+  int S = a->num_splits > 0 ? a->num_splits
+                            : af_decode_num_splits(a->batch, a->heads_q, a->heads_kv, a->seqlen_kv, D);
+  if (max_ws > 0) {
+    const size_t per_split = af_decode_workspace_bytes(a->batch, a->heads_q, D, 1);
+    const size_t fit = max_ws / per_split;
+    if (fit == 0)
+      return fail(AF_ERR_WORKSPACE, "decode partials of one split need %zu bytes, above the %zu-byte limit",
+                  per_split, max_ws);
+    if ((size_t)S > fit) {
+      if (a->num_splits > 0)
+        return fail(AF_ERR_WORKSPACE, "%d splits need %zu bytes of partials, above the %zu-byte limit (at most %zu)",
+                    S, per_split * S, max_ws, fit);
+      S = (int)fit;
+    }
+  }
+  int split_len = (a->seqlen_kv + S - 1) / S;
+  split_len = (split_len + 31) & ~31;
+  S = (a->seqlen_kv + split_len - 1) / split_len;  // drop empty trailing splits
+  *need = af_decode_workspace_bytes(a->batch, a->heads_q, D, S);
+  DecodeParams& p = *out;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.o = static_cast<uint16_t*>(a->o);
+  p.slopes = a->alibi_slopes;
+  for (int i = 0; i < 4; ++i) {
+    p.qs[i] = a->q_stride[i];
+    p.ks[i] = a->k_stride[i];
+    p.vs[i] = a->v_stride[i];
+    p.os[i] = a->o_stride[i];
+  }
+  p.B = a->batch;
+  p.Hq = a->heads_q;
+  p.Hkv = a->heads_kv;
+  p.Nkv = a->seqlen_kv;
+  p.G = a->heads_q / a->heads_kv;
+  p.nqc = (p.G + 15) / 16;
+  p.nsplit = S;
+  p.split_len = split_len;
+  p.scale = a->scale;
+  return AF_OK;
+}
+
+// Split + combine of a planned decode call, with its partials at `workspace`.
+int enqueue_decode(DecodeParams& p, const af_decode_args* a, void* workspace, hipStream_t s) {
+  const size_t rows = (size_t)p.nsplit * p.B * p.Hq;
+  p.ws_ml = static_cast<float*>(workspace);
+  p.ws_acc = p.ws_ml + 2 * rows;
+  const dim3 gs((unsigned)p.nsplit, (unsigned)(p.B * p.Hkv * p.nqc));
+  const dim3 gc((unsigned)(p.B * p.Hq));
+  if (launch_decode(p, a->key.dtype, a->key.head_dim, a->key.bias, gs, gc, s) != 0)
+    return fail(AF_ERR_UNSUPPORTED, "no decode instantiation for this key");
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(AF_ERR_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
+  return AF_OK;
+}
+
 }  // namespace af
 
 using namespace af;
@@ -351,64 +433,14 @@ size_t af_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t head_di
 }
 
 int af_decode(const af_decode_args* a, void* workspace, size_t workspace_bytes, void* stream) {
-  if (a == nullptr) return fail(AF_ERR_BAD_ARG, "args is NULL");
-  int rc;
-  if ((rc = check_bhnd("q", a->q, a->q_stride, 1))) return rc;
-  if ((rc = check_bhnd("k", a->k, a->k_stride, a->seqlen_kv))) return rc;
-  if ((rc = check_bhnd("v", a->v, a->v_stride, a->seqlen_kv))) return rc;
-  if (a->o == nullptr) return fail(AF_ERR_BAD_ARG, "o is NULL");
-  if (a->o_stride[3] != 1) return fail(AF_ERR_BAD_ARG, "o: head-dim stride must be 1");
-  if ((rc = check_key(a->key, false))) return rc;
-  if (a->key.mask != AF_MASK_FULL || a->key.rope != 0 || a->key.norm != AF_NORM_SOFTMAX ||
-      (a->key.bias != AF_BIAS_NONE && a->key.bias != AF_BIAS_ALIBI))
-    return fail(AF_ERR_UNSUPPORTED, "decode takes dense softmax with no bias or ALiBi, no RoPE");
-  if (a->batch <= 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->seqlen_kv <= 0 ||
-      a->heads_q % a->heads_kv != 0)
-    return fail(AF_ERR_BAD_ARG, "bad decode sizes B=%d Hq=%d Hkv=%d Nkv=%d", a->batch, a->heads_q, a->heads_kv,
-                a->seqlen_kv);
-  if (a->key.bias == AF_BIAS_ALIBI && a->alibi_slopes == nullptr) return fail(AF_ERR_BAD_ARG, "ALiBi needs slopes");
-  const int D = a->key.head_dim;
-  int S = a->num_splits > 0 ? a->num_splits
-                            : af_decode_num_splits(a->batch, a->heads_q, a->heads_kv, a->seqlen_kv, D);
-  int split_len = (a->seqlen_kv + S - 1) / S;
-  split_len = (split_len + 31) & ~31;
-  S = (a->seqlen_kv + split_len - 1) / split_len;  // drop empty trailing splits
-  const size_t need = af_decode_workspace_bytes(a->batch, a->heads_q, D, S);
+  DecodeParams p;
+  size_t need = 0;
+  int rc = plan_decode(a, 0, &p, &need);
+  if (rc) return rc;
   if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
     return fail(AF_ERR_WORKSPACE, "decode workspace needs %zu bytes (16-byte aligned), got %zu", need,
                 workspace_bytes);
-  DecodeParams p;
-  memset(&p, 0, sizeof(p));
-  p.q = static_cast<const uint16_t*>(a->q);
-  p.k = static_cast<const uint16_t*>(a->k);
-  p.v = static_cast<const uint16_t*>(a->v);
-  p.o = static_cast<uint16_t*>(a->o);
-  p.slopes = a->alibi_slopes;
-  const size_t rows = (size_t)S * a->batch * a->heads_q;
-  p.ws_ml = static_cast<float*>(workspace);
-  p.ws_acc = p.ws_ml + 2 * rows;
-  for (int i = 0; i < 4; ++i) {
-    p.qs[i] = a->q_stride[i];
-    p.ks[i] = a->k_stride[i];
-    p.vs[i] = a->v_stride[i];
-    p.os[i] = a->o_stride[i];
-  }
-  p.B = a->batch;
-  p.Hq = a->heads_q;
-  p.Hkv = a->heads_kv;
-  p.Nkv = a->seqlen_kv;
-  p.G = a->heads_q / a->heads_kv;
-  p.nqc = (p.G + 15) / 16;
-  p.nsplit = S;
-  p.split_len = split_len;
-  p.scale = a->scale;
-  const dim3 gs((unsigned)S, (unsigned)(a->batch * a->heads_kv * p.nqc));
-  const dim3 gc((unsigned)(a->batch * a->heads_q));
-  if (launch_decode(p, a->key.dtype, D, a->key.bias, gs, gc, static_cast<hipStream_t>(stream)) != 0)
-    return fail(AF_ERR_UNSUPPORTED, "no decode instantiation for this key");
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(AF_ERR_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
-  return AF_OK;
+  return enqueue_decode(p, a, workspace, static_cast<hipStream_t>(stream));
 }
 
 size_t af_bwd_workspace_bytes(const af_bwd_args* args) {

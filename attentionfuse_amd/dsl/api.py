@@ -123,10 +123,26 @@ def attention(fn: Callable) -> Callable:
     return wrapper
 
 
+# Call-time keywords beyond the reference's (bias, cos, sin, block_mask):
+# explicit ALiBi slopes on every route; an output buffer, a saved
+# log-sum-exp and tile-visit counters on the inference forward only.
+_INFERENCE_ONLY_KWARGS = ("out", "save_lse", "coverage")
+
+
 def _route(graph: Graph, Q, K, V, bias, cos, sin, block_mask, kwargs):
     from ..runtime.backward import can_backward
     masks = {m.kind for m in graph.collect_masks()}
     grad = _wants_grad(Q, K, V)
+    unknown = set(kwargs) - {"alibi_slopes", *_INFERENCE_ONLY_KWARGS}
+    if unknown:
+        raise TypeError(f"unexpected keyword arguments {sorted(unknown)}")
+    slopes = kwargs.get("alibi_slopes")
+    autograd = grad and can_backward(graph)
+    if autograd and set(kwargs) & set(_INFERENCE_ONLY_KWARGS):
+        raise ValueError(
+            f"{sorted(set(kwargs) & set(_INFERENCE_ONLY_KWARGS))} are not "
+            "supported when an input requires grad (the autograd path "
+            "allocates its own output and log-sum-exp)")
 
     if MaskKind.BLOCK_SPARSE in masks:
         from ..runtime.block_mask import BlockMask, run_block_sparse_graph
@@ -137,20 +153,27 @@ def _route(graph: Graph, Q, K, V, bias, cos, sin, block_mask, kwargs):
                 "attnfuse.create_block_mask(predicate, Q_LEN, KV_LEN))")
         if not isinstance(block_mask, BlockMask):
             raise TypeError("block_mask must be an attnfuse.BlockMask")
-        if grad and can_backward(graph):
+        if autograd:
             from ..runtime.autograd import AttnFuseFunction
             return AttnFuseFunction.apply(graph, Q, K, V, bias, cos, sin,
-                                          block_mask)
+                                          block_mask, slopes)
         if grad:
             warnings.warn("AttnFuse: no backward for this block-sparse graph; "
                           "the output carries no gradient", stacklevel=3)
+        if kwargs.get("coverage") is not None:
+            raise ValueError("coverage= is taken by the dense/causal/windowed "
+                             "forward; use runtime.run_block_sparse for "
+                             "block-sparse counters")
         return run_block_sparse_graph(graph, Q, K, V, block_mask, cos=cos,
-                                      sin=sin)
+                                      sin=sin, out=kwargs.get("out"),
+                                      save_lse=kwargs.get("save_lse"),
+                                      alibi_slopes=slopes)
 
     if grad:
-        if can_backward(graph):
+        if autograd:
             from ..runtime.autograd import AttnFuseFunction
-            return AttnFuseFunction.apply(graph, Q, K, V, bias, cos, sin, None)
+            return AttnFuseFunction.apply(graph, Q, K, V, bias, cos, sin, None,
+                                          slopes)
         warnings.warn("AttnFuse: this graph is outside the backward scope "
                       "(softmax with full/causal/sliding-window/block-sparse "
                       "masks and none/ALiBi bias); the output carries no "

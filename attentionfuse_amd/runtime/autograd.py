@@ -16,7 +16,8 @@ from .backward import run_backward
 class AttnFuseFunction(torch.autograd.Function):
 
     @staticmethod
-    def forward(ctx, graph, Q, K, V, bias, cos, sin, block_mask=None):
+    def forward(ctx, graph, Q, K, V, bias, cos, sin, block_mask=None,
+                alibi_slopes=None):
         from .dispatch import run_attention
         from .kernel_cache import get_or_compile
         B, Hq, Nq, _ = Q.shape
@@ -25,14 +26,16 @@ class AttnFuseFunction(torch.autograd.Function):
         if block_mask is not None:
             from .block_mask import run_block_sparse_graph
             out = run_block_sparse_graph(graph, Q, K, V, block_mask, cos=cos,
-                                         sin=sin, save_lse=L)
+                                         sin=sin, save_lse=L,
+                                         alibi_slopes=alibi_slopes)
         else:
             out = run_attention(graph, Q, K, V, bias=bias, cos=cos, sin=sin,
-                                save_lse=L)
+                                save_lse=L, alibi_slopes=alibi_slopes)
         ctx.graph = graph
         ctx.sm_scale = bundle.sm_scale
         ctx.block_mask = block_mask
         ctx.rope = (cos, sin) if bundle.has_rope else (None, None)
+        ctx.alibi_slopes = alibi_slopes if bundle.bias_kind == 1 else None
         ctx.save_for_backward(Q, K, V, out, L)
         return out
 
@@ -42,8 +45,9 @@ class AttnFuseFunction(torch.autograd.Function):
         cos, sin = ctx.rope
         dQ, dK, dV = run_backward(ctx.graph, Q, K, V, O, L, dO.contiguous(),
                                   ctx.sm_scale, cos=cos, sin=sin,
-                                  block_mask=ctx.block_mask)
-        return None, dQ, dK, dV, None, None, None, None
+                                  block_mask=ctx.block_mask,
+                                  alibi_slopes=ctx.alibi_slopes)
+        return None, dQ, dK, dV, None, None, None, None, None
 
 
 class AttnFuseBlockSparseFunction(torch.autograd.Function):

@@ -175,9 +175,10 @@ def run_block_sparse(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
 
 
 def run_block_sparse_graph(graph, Q, K, V, block_mask: BlockMask, *, cos=None,
-                           sin=None, out=None, save_lse=None):
-    """Block-sparse forward of a traced graph, honouring its scale, ALiBi and
-    RoPE."""
+                           sin=None, out=None, save_lse=None,
+                           alibi_slopes=None):
+    """Block-sparse forward of a traced graph, honouring its scale, ALiBi
+    (default slopes or ``alibi_slopes``) and RoPE."""
     from .kernel_cache import get_or_compile
     bundle = get_or_compile(graph)
     if bundle.bias_kind == 2:
@@ -189,7 +190,8 @@ def run_block_sparse_graph(graph, Q, K, V, block_mask: BlockMask, *, cos=None,
                             bias_kind=bundle.bias_kind, out=out,
                             save_lse=save_lse,
                             cos=cos if bundle.has_rope else None,
-                            sin=sin if bundle.has_rope else None)
+                            sin=sin if bundle.has_rope else None,
+                            alibi_slopes=alibi_slopes)
 
 
 def run_block_sparse_backward(Q, K, V, O, L, dO, block_mask: BlockMask,

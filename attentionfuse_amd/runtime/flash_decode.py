@@ -5,22 +5,22 @@ attnfuse/runtime/flash_decode.py:46-187): ``Q.N == 1``, ``N_kv >= 256``,
 dense mask, no bias or ALiBi, no RoPE -- plus softmax normalisation (the
 reference also routes ReLU graphs here and then computes a softmax).
 
-The split workspace is caller-provided at the C ABI; here it comes from a
-per-device buffer that only grows, so steady-state decoding allocates
-nothing per call (the reference allocates three workspaces per call,
-flash_decode.py:134-139).
+The split workspace is caller-provided at the C ABI.  Here it is one
+allocation per call from torch's caching allocator on the current stream, as
+the reference allocates its three workspaces per call
+(flash_decode.py:134-139): the block is stream-ordered, so concurrent calls
+on different streams never share partials, a call under graph capture draws
+from the graph's private pool, and freeing it after the launch is safe.
+Fixed-shape loops that want no per-call allocation use
+``prepared.prepare_decode`` (its own workspace) or the C entry point
+``af_decode_noalloc``.
 """
 from __future__ import annotations
-
-import threading
 
 import torch
 
 from ..ir.high_level import BiasKind, Graph, MaskKind, NormKind
 from . import _native as N
-
-_ws_lock = threading.Lock()
-_workspaces: dict = {}
 
 
 def can_use_flash_decode(graph: Graph, Q: torch.Tensor, K: torch.Tensor) -> bool:
@@ -42,15 +42,9 @@ def _pick_num_splits(B: int, H_q: int, N_kv: int, H_kv: int | None = None,
 
 
 def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A cached per-device byte buffer of at least ``nbytes``."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    with _ws_lock:
-        buf = _workspaces.get(idx)
-        if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8,
-                              device=device)
-            _workspaces[idx] = buf
-        return buf
+    """A fresh ``nbytes`` byte buffer from torch's caching allocator, owned
+    by the current stream of ``device``."""
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
 
 
 def run_flash_decode(graph: Graph, Q: torch.Tensor, K: torch.Tensor,

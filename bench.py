@@ -32,10 +32,17 @@ HBM, every step exactly one kernel launch.  The same line carries
   B=1 N=4096 H_q=32 H_kv=8 D=128): 3.5 x 4*B*H_q*D*N(N+1)/2 FLOP per step;
 * ``train_fp32`` -- config 5 on fp32 inputs, against the fp32 MFMA peak;
 * ``cpu_baseline`` -- the fp32 CPU oracle (a restatement of the reference's
-  naive attention) on a bounded sample of config 2's heads, on the host's
-  cores, plus config 1 (GPT-2-small causal, B=1 H=12 N=512 D=64, fp32) in
-  full, and the max-abs difference between the GPU output and the oracle on
-  the sampled heads.
+  naive attention) on a bounded sample of config 2's heads, on every core of
+  the process's affinity set (bounded by OMP_NUM_THREADS where the host sets
+  it), with the CPU model, plus config 1 (GPT-2-small causal, B=1 H=12 N=512
+  D=64, fp32) in full;
+* ``parity`` on the line and on every sub-line -- the timed launch's outputs
+  (and gradients) against the fp32 CPU oracle on a sample of heads: max-abs
+  error of outputs, ||g - g_ref||_F / ||g_ref||_F of gradients, with the
+  tolerance each must meet.  ``--no-cpu`` skips the oracle and the parity.
+
+Peaks are the published MI355X figures: 2.5 PFLOP/s dense fp16/bf16 MFMA,
+157.3 TFLOP/s dense fp32 MFMA, 8 TB/s HBM3E.
 """
 from __future__ import annotations
 
@@ -156,13 +163,15 @@ def bench_decode(steps, warmup):
         V = torch.randn(B, Hkv, N, D, generator=g, device=dev, dtype=torch.bfloat16)
         sets.append((Q, K, V))
     graph = dense(*sets[0], return_graph=True)
-    launches = [prepare_decode(graph, *s)[0] for s in sets]
+    prepared = [prepare_decode(graph, *s) for s in sets]
+    launches = [p[0] for p in prepared]
     state = {"i": 0}
 
     def launch():
         launches[state["i"] & 1]()
         state["i"] += 1
-    return _time_launch(launch, steps, warmup)
+    ms = _time_launch(launch, steps, warmup)
+    return ms, (sets[0], prepared[0][1])
 
 
 def bench_decode_latency(steps, warmup):
@@ -223,16 +232,19 @@ def bench_bigbird(steps, warmup):
     out = torch.empty_like(Q)
     scale = D ** -0.5
 
+    grads = {}
+
     def step():
         run_block_sparse(Q, K, V, bm, scale, out=out, save_lse=L)
-        run_block_sparse_backward(Q, K, V, out, L, dO, bm, scale)
+        grads["g"] = run_block_sparse_backward(Q, K, V, out, L, dO, bm, scale)
     ms = _time_launch(step, steps, warmup)
     flops = 14 * B * H * D * 64 * 64 * bm.n_active
-    return {"workload": "config 4: BigBird block-sparse fwd+bwd fp16 B=4 H=12 N=4096 D=64, "
-                        f"64x64 blocks, {bm.n_active} active of {n * n}",
-            "ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
-            "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
-            "algorithmic_flop_per_step": flops}
+    res = {"workload": "config 4: BigBird block-sparse fwd+bwd fp16 B=4 H=12 N=4096 D=64, "
+                       f"64x64 blocks, {bm.n_active} active of {n * n}",
+           "ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+           "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+           "algorithmic_flop_per_step": flops}
+    return res, (Q, K, V, dO, out) + tuple(grads["g"]) + (grid,)
 
 
 def bench_train(steps, warmup, dtype=None):
@@ -259,18 +271,21 @@ def bench_train(steps, warmup, dtype=None):
     fwd, out = prepare_attention(graph, Q, K, V, cos=cos, sin=sin, save_lse=L)
     scale = D ** -0.5
 
+    grads = {}
+
     def step():
         fwd()
-        run_backward(graph, Q, K, V, out, L, dO, scale, cos=cos, sin=sin)
+        grads["g"] = run_backward(graph, Q, K, V, out, L, dO, scale, cos=cos, sin=sin)
     ms = _time_launch(step, steps, warmup)
     flops = int(3.5 * causal_flops(B, Hq, N, D))
     f32 = dtype == torch.float32
     peak = PEAK_FP32_TFLOPS if f32 else PEAK_FP16_TFLOPS
-    return {"workload": "config 5: causal GQA + RoPE(base 5e5) fwd+bwd %s "
-                        "B=1 N=4096 Hq=32 Hkv=8 D=128" % ("fp32" if f32 else "bf16"),
-            "ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
-            "frac": round(flops / (ms * 1e-3) / 1e12 / peak, 4),
-            "algorithmic_flop_per_step": flops}
+    res = {"workload": "config 5: causal GQA + RoPE(base 5e5) fwd+bwd %s "
+                       "B=1 N=4096 Hq=32 Hkv=8 D=128" % ("fp32" if f32 else "bf16"),
+           "ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+           "frac": round(flops / (ms * 1e-3) / 1e12 / peak, 4),
+           "algorithmic_flop_per_step": flops}
+    return res, (Q, K, V, dO, out) + tuple(grads["g"]) + (cos, sin)
 
 
 def copy_calibration(reps=5):
@@ -307,6 +322,27 @@ def load_traffic(kernels):
     return None, None
 
 
+def _cpu_model():
+    """The host CPU's model name (what lscpu prints as "Model name")."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_threads():
+    """(threads used, cores in this process's affinity set): every core the
+    process may run on, bounded by OMP_NUM_THREADS when the host sets it (the
+    GPU boxes give one GPU's job a share of the host's cores that way)."""
+    aff = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    n = min(aff, int(omp)) if omp.isdigit() and int(omp) > 0 else aff
+    return n, aff
+
+
 def cpu_baseline(tensors, budget_s=10.0, max_heads=48):
     """fp32 CPU oracle on whole (b, h) heads of config 2 until the time budget
     is spent; returns throughput in algorithmic TFLOP/s and parity."""
@@ -315,7 +351,7 @@ def cpu_baseline(tensors, budget_s=10.0, max_heads=48):
     import oracle as O
     Q, K, V, cos, sin, out = tensors
     B, H, N, D = Q.shape
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores, aff = _cpu_threads()
     torch.set_num_threads(cores)
     c, s = cos[0, 0].cpu(), sin[0, 0].cpu()
     done, t_total, err = 0, 0.0, 0.0
@@ -332,8 +368,84 @@ def cpu_baseline(tensors, budget_s=10.0, max_heads=48):
     flops = causal_flops(1, done, N, D)
     return {"value": round(flops / t_total / 1e12, 6), "unit": "TFLOPS",
             "cores": cores, "kind": "port",
+            "cpu_model": _cpu_model(), "affinity_cores": aff,
             "sample": f"{done} of {B * H} (b,h) heads of config 2 (causal+RoPE, "
                       f"N={N}, D={D}), fp32 torch on CPU, {t_total:.2f} s"}, err
+
+
+# ---------------------------------------------------------------------------
+# Parity of each timed launch against the fp32 CPU oracle, on a sample of
+# heads (the full problems take minutes on the CPU).  Output error is
+# max-abs; gradient error is ||g - g_ref||_F / ||g_ref||_F per tensor.
+# ---------------------------------------------------------------------------
+def _rel(a, b):
+    return float((a.float().cpu() - b.float()).norm() / b.float().norm())
+
+
+def parity_forward(tensors, alibi, heads=((0, 0), (1, 5), (2, 7), (3, 11))):
+    import torch
+
+    import oracle as O
+    Q, K, V, cos, sin, out = tensors
+    H = Q.shape[1]
+    rope = (cos[0, 0].cpu(), sin[0, 0].cpu())
+    slopes = torch.tensor([2.0 ** (-8.0 * (h + 1) / H) for h in range(H)])
+    err = 0.0
+    for b, h in heads:
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        want = O.naive_attention(Q[sl].cpu(), K[sl].cpu(), V[sl].cpu(), causal=True, rope=rope,
+                                 alibi_slopes=slopes[h:h + 1] if alibi else None)
+        err = max(err, (out[sl].float().cpu() - want).abs().max().item())
+    tol = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2, torch.float32: 3e-5}[Q.dtype]
+    return {"max_abs": err, "tol": tol, "sample": f"(b,h) in {list(heads)}"}
+
+
+def parity_decode(tensors, batches=(0, 7)):
+    import oracle as O
+    (Q, K, V), out = tensors
+    err = 0.0
+    for b in batches:
+        want = O.naive_attention(Q[b:b + 1].cpu(), K[b:b + 1].cpu(), V[b:b + 1].cpu())
+        err = max(err, (out[b:b + 1].float().cpu() - want).abs().max().item())
+    return {"max_abs": err, "tol": 1.6e-2, "sample": f"batches {list(batches)}, all 32 query heads"}
+
+
+def parity_bigbird(tensors, heads=((0, 0), (3, 11))):
+    import torch
+
+    import oracle as O
+    Q, K, V, dO, out, dQ, dK, dV, grid = tensors
+    N = Q.shape[2]
+    mask = O.element_mask_from_grid(grid, N, N, 64, 64)
+    res = {"max_abs": 0.0, "grad_rel": 0.0}
+    for b, h in heads:
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        o, dq, dk, dv = O.attention_grads(Q[sl], K[sl], V[sl], dO[sl], dtype=torch.float32,
+                                          elem_mask=mask)
+        res["max_abs"] = max(res["max_abs"], (out[sl].float().cpu() - o).abs().max().item())
+        res["grad_rel"] = max(res["grad_rel"], _rel(dQ[sl], dq), _rel(dK[sl], dk), _rel(dV[sl], dv))
+    res.update(tol=2e-3, grad_tol=1e-2, sample=f"(b,h) in {list(heads)}, fwd O and dQ/dK/dV")
+    return res
+
+
+def parity_train(tensors, kv_heads=(0,)):
+    import torch
+
+    import oracle as O
+    Q, K, V, dO, out, dQ, dK, dV, cos, sin = tensors
+    G = Q.shape[1] // K.shape[1]
+    rope = (cos[0, 0].cpu(), sin[0, 0].cpu())
+    res = {"max_abs": 0.0, "grad_rel": 0.0}
+    for hk in kv_heads:
+        qs, ks = slice(G * hk, G * (hk + 1)), slice(hk, hk + 1)
+        o, dq, dk, dv = O.attention_grads(Q[:, qs], K[:, ks], V[:, ks], dO[:, qs],
+                                          dtype=torch.float32, causal=True, rope=rope)
+        res["max_abs"] = max(res["max_abs"], (out[:, qs].float().cpu() - o).abs().max().item())
+        res["grad_rel"] = max(res["grad_rel"], _rel(dQ[:, qs], dq), _rel(dK[:, ks], dk), _rel(dV[:, ks], dv))
+    tol = 3e-5 if Q.dtype == torch.float32 else 1.6e-2
+    res.update(tol=tol, grad_tol=1e-2,
+               sample=f"KV heads {list(kv_heads)} with their {G} query heads, O and dQ/dK/dV")
+    return res
 
 
 def cpu_config1(iters=10, warm=3):
@@ -419,8 +531,10 @@ def main():
                      "algorithmic_flop_per_launch": flops,
                      "algorithmic_bytes_per_launch": 4 * C2["B"] * C2["H"] * C2["N"] * C2["D"] * 2},
     }
+    checks = {}   # sub-line -> (parity function, tensors); run with the CPU leg
     if not args.no_alibi:
-        ms_alibi, _ = bench_forward(args.steps, args.warmup, alibi=True)
+        ms_alibi, t_alibi = bench_forward(args.steps, args.warmup, alibi=True)
+        checks["alibi"] = (lambda t=t_alibi: parity_forward(t, alibi=True))
         tflops_alibi = flops / (ms_alibi * 1e-3) / 1e12
         line["alibi"] = {"workload": "config 2 as written: causal+RoPE+ALiBi forward, fp16, "
                                      "B=4 H=12 N=4096 D=64",
@@ -429,14 +543,16 @@ def main():
                          "slopes": "2^(-8(h+1)/H), h=0..11 (config 2 as written)"}
     if not args.no_fp32:
         import torch
-        ms_f32, _ = bench_forward(args.steps, args.warmup, alibi=False, dtype=torch.float32)
+        ms_f32, t_f32 = bench_forward(args.steps, args.warmup, alibi=False, dtype=torch.float32)
+        checks["fp32"] = (lambda t=t_f32: parity_forward(t, alibi=False))
         tflops_f32 = flops / (ms_f32 * 1e-3) / 1e12
         line["fp32"] = {"workload": "config 2's causal+RoPE forward on fp32 inputs, B=4 H=12 N=4096 D=64",
                         "ms": round(ms_f32, 5), "tflops": round(tflops_f32, 3), "bound": "mfma",
                         "peak": PEAK_FP32_TFLOPS,
                         "frac": round(tflops_f32 / PEAK_FP32_TFLOPS, 4)}
     if not args.no_decode:
-        ms_dec = bench_decode(args.steps, args.warmup)
+        ms_dec, t_dec = bench_decode(args.steps, args.warmup)
+        checks["decode"] = (lambda t=t_dec: parity_decode(t))
         nbytes = decode_bytes(**{k: C3[k] for k in ("B", "Hq", "Hkv", "N", "D")})
         gbs = nbytes / (ms_dec * 1e-3) / 1e9
         line["decode"] = {"workload": "config 3: GQA decode bf16 B=8 Hq=32 Hkv=8 D=128 cache 32768",
@@ -446,16 +562,23 @@ def main():
                           "algorithmic_bytes_per_launch": nbytes}
         line["decode_latency"] = bench_decode_latency(args.steps, args.warmup)
     if not args.no_train:
-        line["bigbird"] = bench_bigbird(max(args.steps // 2, 1), max(args.warmup // 2, 1))
-        line["train"] = bench_train(max(args.steps // 2, 1), max(args.warmup // 2, 1))
+        line["bigbird"], t_bb = bench_bigbird(max(args.steps // 2, 1), max(args.warmup // 2, 1))
+        checks["bigbird"] = (lambda t=t_bb: parity_bigbird(t))
+        line["train"], t_tr = bench_train(max(args.steps // 2, 1), max(args.warmup // 2, 1))
+        checks["train"] = (lambda t=t_tr: parity_train(t))
         if not args.no_fp32:
             import torch
-            line["train_fp32"] = bench_train(max(args.steps // 5, 1), 1, dtype=torch.float32)
+            line["train_fp32"], t_tr32 = bench_train(max(args.steps // 5, 1), 1, dtype=torch.float32)
+            checks["train_fp32"] = (lambda t=t_tr32: parity_train(t))
     if not args.no_cpu:
         cb, err = cpu_baseline(tensors)
         line["cpu_baseline"] = cb
         line["cpu_config1"] = cpu_config1()
         line["parity_max_abs_vs_oracle"] = err
+        line["parity"] = {"max_abs": err, "tol": 2e-3,
+                          "sample": cb["sample"].split(" (")[0] + " (the cpu_baseline heads)"}
+        for name, fn in checks.items():
+            line[name]["parity"] = fn()
     line["wall_s"] = round(time.time() - t_wall, 1)
     print(json.dumps(line), flush=True)
 

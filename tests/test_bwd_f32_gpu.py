@@ -77,6 +77,16 @@ def test_backward_gqa_group_sum(name):
     run(name, 2, 8, 2, 192, 64)
 
 
+@pytest.mark.parametrize("D", [32, 128])
+@pytest.mark.parametrize("name", ["causal", "rope_causal_alibi"])
+def test_backward_gqa_split_head_dims(name, D):
+    """GQA group of 4 at D=128 (config 5's ratio) and D=32: the group is
+    split over several dK/dV workgroups whose partials the combine kernel
+    adds, at every head dim."""
+    print(f"[bwd f32] {name} GQA 8/2 D={D}", flush=True)
+    run(name, 1, 8, 2, 384, D)
+
+
 @pytest.mark.parametrize("Nq,Nkv", [(64, 0), (0, 64), (1, 0)])
 def test_backward_with_an_empty_side(Nq, Nkv):
     """No keys: O = 0 and dQ = 0; no queries: dK = dV = 0."""

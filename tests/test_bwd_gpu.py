@@ -155,3 +155,22 @@ def test_backward_with_an_empty_side(Nq, Nkv):
     for t in (q, k, v):
         assert t.grad is not None and t.grad.shape == t.shape
         assert torch.count_nonzero(t.grad) == 0
+
+
+def test_explicit_alibi_slopes_reach_the_backward():
+    """alibi_slopes= on a call that requires grad is used by the forward and
+    the backward (config 2's slopes 2^(-8(h+1)/H), which differ from the
+    default recipe at H=12)."""
+    B, H, N, D = 1, 12, 256, 64
+    dtype = torch.float16
+    g = torch.Generator(device="cuda").manual_seed(11)
+    Q, K, V, dO = (torch.randn(B, H, N, D, generator=g, device="cuda", dtype=dtype) for _ in range(4))
+    slopes = torch.tensor([2.0 ** (-8.0 * (h + 1) / H) for h in range(H)])
+    q, k, v = (t.clone().requires_grad_(True) for t in (Q, K, V))
+    out = _fn("causal_alibi", H)(q, k, v, alibi_slopes=slopes.cuda())
+    out.backward(dO)
+    torch.cuda.synchronize()
+    o_ref, dq, dk, dv = O.attention_grads(Q.cpu(), K.cpu(), V.cpu(), dO.cpu(), dtype=torch.float32,
+                                          causal=True, alibi_slopes=slopes)
+    check({"O": (out.detach().float().cpu() - o_ref).abs().max().item(),
+           "dQ": rel(q.grad, dq), "dK": rel(k.grad, dk), "dV": rel(v.grad, dv)}, dtype)

@@ -87,3 +87,27 @@ def test_llama3_8b_geometry_small_batch():
     torch.cuda.synchronize()
     want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu())
     assert (out.float().cpu() - want).abs().max().item() <= TOL[torch.bfloat16]
+
+
+def test_concurrent_decodes_on_two_streams():
+    """Two decode calls in flight at once on two streams, each with its own
+    split partials (the Python route allocates them per call from the
+    stream's allocator pool); both match the oracle."""
+    a = make(4, 32, 8, 16384, 128, torch.bfloat16, seed=21)
+    b = make(2, 8, 2, 9000, 64, torch.float16, seed=22)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for s in (s1, s2):
+        s.wait_stream(torch.cuda.current_stream())
+    outs = {}
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            outs["a"] = dense(*a)
+        with torch.cuda.stream(s2):
+            outs["b"] = dense(*b)
+    for s in (s1, s2):
+        torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for name, (Q, K, V), dt in (("a", a, torch.bfloat16), ("b", b, torch.float16)):
+        want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu())
+        err = (outs[name].float().cpu() - want).abs().max().item()
+        assert err <= TOL[dt], (name, err)

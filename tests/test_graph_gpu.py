@@ -1,15 +1,18 @@
-"""Prepared launches captured in a HIP graph (torch.cuda.CUDAGraph) give the
-same bytes as eager launches on every replay.
+"""Prepared launches, eager and captured in a HIP graph (torch.cuda.CUDAGraph),
+against the fp32 CPU oracle.
 
 The kernels allocate nothing, take caller-owned workspaces and record no
 memset, so a serving loop can capture a decode step or a prefill once and
 replay it.  Each graph is replayed several times with other eager work and
-synchronisations in between, and every replay is compared with the eager
-result of the same launch."""
+synchronisations in between; every replay must equal the eager launch bit for
+bit and the oracle within the forward tolerances (2e-3 fp16, 1.6e-2 bf16).
+New input values written into the captured storage between replays must
+give the oracle's answer for the new values."""
 import pytest
 import torch
 
 import attnfuse as af
+import oracle as O
 from attnfuse.rope_utils import build_rope_cache
 from attentionfuse_amd.runtime.prepared import prepare_attention, prepare_decode
 
@@ -30,7 +33,7 @@ def _capture(launch):
     return graph
 
 
-def _replays_match(graph, out, want, scratch):
+def _replays_match(graph, out, want, scratch, oracle_out, tol):
     for i in range(4):
         out.zero_()
         scratch.mul_(1.5).add_(float(i))   # unrelated eager work between replays
@@ -38,6 +41,8 @@ def _replays_match(graph, out, want, scratch):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, want), f"replay {i} differs from the eager launch"
+        err = (out.float().cpu() - oracle_out).abs().max().item()
+        assert err <= tol, f"replay {i}: max|err| vs oracle {err:.3e}"
 
 
 @pytest.mark.parametrize("rope", [False, True], ids=["plain", "rope"])
@@ -55,8 +60,19 @@ def test_forward_graph_replays_match_eager(rope):
     launch()
     torch.cuda.synchronize()
     want = out.clone()
+    rope_t = (cos[0, 0].cpu(), sin[0, 0].cpu()) if rope else None
+    ref = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(), causal=True, rope=rope_t)
+    assert (want.float().cpu() - ref).abs().max().item() <= 2e-3
     graph = _capture(launch)
-    _replays_match(graph, out, want, torch.ones(1 << 16, device="cuda"))
+    _replays_match(graph, out, want, torch.ones(1 << 16, device="cuda"), ref, 2e-3)
+    # new values in the captured storage: the replay computes on them
+    g2 = torch.Generator(device="cuda").manual_seed(4)
+    for t in (Q, K, V):
+        t.copy_(torch.randn(t.shape, generator=g2, device="cuda", dtype=t.dtype))
+    graph.replay()
+    torch.cuda.synchronize()
+    ref2 = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(), causal=True, rope=rope_t)
+    assert (out.float().cpu() - ref2).abs().max().item() <= 2e-3
 
 
 def test_decode_graph_replays_match_eager():
@@ -71,5 +87,13 @@ def test_decode_graph_replays_match_eager():
     launch()
     torch.cuda.synchronize()
     want = out.clone()
+    ref = O.naive_attention(Q.cpu(), K.cpu(), V.cpu())
+    assert (want.float().cpu() - ref).abs().max().item() <= 1.6e-2
     graph = _capture(launch)
-    _replays_match(graph, out, want, torch.ones(1 << 16, device="cuda"))
+    _replays_match(graph, out, want, torch.ones(1 << 16, device="cuda"), ref, 1.6e-2)
+    # a new query token in the captured storage
+    Q.copy_(torch.randn(Q.shape, generator=g, device="cuda", dtype=Q.dtype))
+    graph.replay()
+    torch.cuda.synchronize()
+    ref2 = O.naive_attention(Q.cpu(), K.cpu(), V.cpu())
+    assert (out.float().cpu() - ref2).abs().max().item() <= 1.6e-2

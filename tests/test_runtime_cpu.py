@@ -104,3 +104,15 @@ def test_block_sparse_mask_errors():
         bs(q, q, q)
     with pytest.raises(TypeError):
         bs(q, q, q, block_mask=object())
+
+
+def test_call_keywords_are_checked_before_any_launch():
+    """Unknown call-time keywords raise TypeError; inference-only buffers
+    (out=, save_lse=, coverage=) with an input that requires grad raise
+    ValueError instead of being dropped by the autograd route."""
+    z = torch.zeros(1, 2, 16, 64, dtype=torch.float16)
+    with pytest.raises(TypeError):
+        causal(z, z, z, bogus=1)
+    zq = z.clone().requires_grad_(True)
+    with pytest.raises(ValueError):
+        causal(zq, z, z, out=torch.empty_like(z))
