@@ -102,6 +102,7 @@ SIGNATURES = {
     "af_decode_workspace_bytes": (C.c_size_t, [C.c_int32] * 4),
     "af_decode": (C.c_int, [C.POINTER(DecodeArgsC), C.c_void_p, C.c_size_t,
                             C.c_void_p]),
+    "af_decode_noalloc": (C.c_int, [C.POINTER(DecodeArgsC), C.c_void_p]),
     "af_bwd_workspace_bytes": (C.c_size_t, [C.POINTER(BwdArgsC)]),
     "af_bwd": (C.c_int, [C.POINTER(BwdArgsC), C.POINTER(BlockMaskC),
                          C.c_void_p, C.c_size_t, C.c_void_p]),

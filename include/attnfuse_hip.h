@@ -160,6 +160,21 @@ size_t af_decode_workspace_bytes(int32_t batch, int32_t heads_q,
 int af_decode(const af_decode_args* args, void* workspace,
               size_t workspace_bytes, void* stream);
 
+/* Flash decoding that allocates nothing and takes no workspace.  It has no
+ * counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops that forbid
+ * hipMalloc).  The split partials live in a library-owned device array of
+ * AF_DECODE_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on that
+ * GPU until the process ends.  With num_splits <= 0 the split count is
+ * lowered until the partials fit; an explicit num_splits, or a batch whose
+ * single-split partials (B * H_q * (2 + D) * 4 bytes) do not fit, returns
+ * AF_ERR_WORKSPACE.  Every call on one GPU shares the array: calls that
+ * overlap in time on one GPU (other streams, other threads) race; calls on
+ * one stream are ordered.  Results equal af_decode's for the same split
+ * count. */
+#define AF_DECODE_NOALLOC_SCRATCH_BYTES (4u << 20)
+int af_decode_noalloc(const af_decode_args* args, void* stream);
+
 /* Backward (FA2 style: delta = rowsum(dO*O), then dK/dV, then dQ).
  * Replaces attnfuse_bwd_{preproc,dkv,dq}_kernel and the block-sparse dkv/dq
  * kernels (reference: attnfuse/runtime/backward.py:83-192,
