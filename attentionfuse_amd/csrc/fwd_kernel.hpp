@@ -245,6 +245,31 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
       for (int ks = 0; ks < KS; ++ks) s[kb] = E::mfma32(ld16(Ks + 32 * kb * D + koff[ks]), qf[ks], s[kb]);
     }
   };
+  // The same in two parts, for head dims whose operands fit in registers
+  // next to the scores: every K operand of a tile is read from LDS first, so
+  // that the MFMAs, issued later, find them landed instead of each waiting
+  // out one LDS round trip.
+  constexpr bool kBatchK = D <= 64;
+  constexpr bool kBatchV = D <= 64;
+  // The first key block's operands are read up front; the second block's
+  // are read as the first block's MFMAs issue.
+  auto read_k = [&](int par, u32x4 (&kop)[KS]) {
+    const uint16_t* Ks = lds + par * TILE;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kop[ks] = ld16(Ks + koff[ks]);
+  };
+  auto scores_k = [&](int par, const u32x4 (&kop)[KS], f32x16* s) {
+    const uint16_t* Ks = lds + par * TILE;
+    s[0] = sinit;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) s[0] = E::mfma32(kop[ks], qf[ks], s[0]);
+#pragma unroll
+    for (int kb = 1; kb < BN / 32; ++kb) {
+      s[kb] = sinit;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) s[kb] = E::mfma32(ld16(Ks + 32 * kb * D + koff[ks]), qf[ks], s[kb]);
+    }
+  };
 
   // S^T of tile t recomputed from K in global memory, for the rare step that
   // must move the running max after its K slot has been refilled.  Same
@@ -463,17 +488,56 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
       }
     }
   };
+  // Pipelined form: the V^T operands are read kVAhead MFMAs ahead of the
+  // MFMA that consumes them (read one by one, each MFMA waited out the LDS
+  // round trip of its own transposing reads).  The scheduling barriers keep
+  // the compiler from sinking each read back next to its MFMA.
+  constexpr int kVOps = DB * (BN / 16);
+  constexpr int kVAhead = kVOps < 4 ? kVOps : 4;
+  auto read_vop = [&](int par, int i) -> u32x4 {
+    const int kk = i / DB, db = i % DB;
+    const uint16_t* vt = lds + (2 + par) * TILE + 16 * kk * D;
+    const u32x2 lo = lds_read_tr16(vt + voff[db][0]);
+    const u32x2 hi = lds_read_tr16(vt + voff[db][1]);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  };
+  auto pv_pipe = [&](int par, const u32x4* pf) {
+    u32x4 vop[kVOps];
+#pragma unroll
+    for (int i = 0; i < kVAhead; ++i) vop[i] = read_vop(par, i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kVOps; ++i) {
+      const int kk = i / DB, db = i % DB;
+      o[db] = E::mfma32(vop[i], pf[kk], o[db]);
+      if (i + kVAhead < kVOps) vop[i + kVAhead] = read_vop(par, i + kVAhead);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
 
   // One step with the running max computed first (every step for relu and
   // ALiBi; the first step otherwise): bias, mask and max of tile t, then the score
   // MFMAs of tile t+1 in the same basic block as P of tile t, and P V(t).
   auto step_exact = [&](int t, int par, f32x16* s, f32x16* nxt) {
+    u32x4 kop[KS];
+    if constexpr (kBatchK) {
+      read_k(par ^ 1, kop);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     const Logit lg = rebase(s, bias_mask(t, s, true));
-    scores(par ^ 1, nxt);
+    if constexpr (kBatchK) {
+      scores_k(par ^ 1, kop, nxt);
+    } else {
+      scores(par ^ 1, nxt);
+    }
     u32x4 pf[BN / 16];
     softmax_tile(s, lg, pf);
     add_rowsum(pf);
-    pv(par, pf);
+    if constexpr (kBatchV) {
+      pv_pipe(par, pf);
+    } else {
+      pv(par, pf);
+    }
   };
 
   // Later softmax steps skip the max: P is taken against the current
@@ -487,11 +551,20 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // the max (16 v_max3, a lane swap and the compare) on almost every tile.
   constexpr float kRedo = 8192.f;  // 2^13
   auto step_lazy = [&](int t, int par, f32x16* s, f32x16* nxt) {
+    u32x4 kop[KS];
+    if constexpr (kBatchK) {
+      read_k(par ^ 1, kop);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     const Logit lg0 = bias_mask(t, s, true);
     Logit lg = lg0;
 #pragma unroll
     for (int kb = 0; kb < BN / 32; ++kb) lg.off[kb] -= m_run;
-    scores(par ^ 1, nxt);
+    if constexpr (kBatchK) {
+      scores_k(par ^ 1, kop, nxt);
+    } else {
+      scores(par ^ 1, nxt);
+    }
     u32x4 pf[BN / 16];
     softmax_tile(s, lg, pf);
     float tsum = tile_rowsum(pf);
@@ -502,7 +575,11 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
       tsum = tile_rowsum(pf);
     }
     lsum[0] += tsum;
-    pv(par, pf);
+    if constexpr (kBatchV) {
+      pv_pipe(par, pf);
+    } else {
+      pv(par, pf);
+    }
   };
 
   // ---- software pipeline ---------------------------------------------------
