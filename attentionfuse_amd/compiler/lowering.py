@@ -19,7 +19,7 @@ import math
 from ..ir.high_level import Graph, MaskKind, ScoreKind
 from ..ir.spec import SpecKey
 from .fusion import fuse_score_softmax
-from .tiling import choose_tile_config
+from .tiling import tile_for_key
 
 
 def lower_to_key(graph: Graph) -> SpecKey:
@@ -51,12 +51,14 @@ def lower_to_key(graph: Graph) -> SpecKey:
     bias_kind = biases[0].kind if biases else None
     bias_heads = biases[0].num_heads if biases else None
 
-    return SpecKey(
+    key = SpecKey(
         head_dim=head_dim, dtype=graph.q.dtype, score_scale=float(scale),
         mask_kind=mask_kind, mask_window=window, bias_kind=bias_kind,
         bias_num_heads=bias_heads, norm_kind=graph.norm().kind,
-        rope_kind=1 if score.rope else 0, config=choose_tile_config(graph),
-        cache_key=graph.signature())
+        rope_kind=1 if score.rope else 0, cache_key=graph.signature())
+    # the launch shape the library uses for this key (single source)
+    key.config = tile_for_key(key.abi_tuple())
+    return key
 
 
 # Reference name of the lowering entry point.

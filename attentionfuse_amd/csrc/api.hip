@@ -8,6 +8,7 @@
 #include <algorithm>
 
 #include "attnfuse_hip.h"
+#include "bwd_f32_kernel.hpp"
 #include "bwd_launch.hpp"
 #include "fwd_f32_kernel.hpp"
 #include "launch.hpp"
@@ -450,6 +451,26 @@ size_t af_bwd_workspace_bytes(const af_bwd_args* args) {
 int af_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_t workspace_bytes,
            void* stream) {
   return run_bwd(a, bm, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int af_bwd_tile(const af_bwd_args* a, const af_blockmask* bm, int32_t* block_m, int32_t* block_n,
+                int32_t* group_split) {
+  if (a == nullptr) return fail(AF_ERR_BAD_ARG, "args is NULL");
+  if (!group_split_valid(*a))
+    return fail(AF_ERR_BAD_ARG, "group_split must be 0 or a power of two dividing heads_q / heads_kv");
+  // dQ: 4 waves x 32 query rows; dK/dV: 4 waves x 32 keys (the fp32
+  // kernels: kBwdF32Block of each); block-sparse launches follow the mask's
+  // blocks
+  int bm_rows = 128, bn_keys = 128;
+  if (a->key.dtype == AF_F32) bm_rows = bn_keys = kBwdF32Block;
+  if (a->key.mask == AF_MASK_BLOCK_SPARSE && bm != nullptr) {
+    bm_rows = bm->block_m;
+    bn_keys = bm->block_n;
+  }
+  if (block_m) *block_m = bm_rows;
+  if (block_n) *block_n = bn_keys;
+  if (group_split) *group_split = a->key.dtype == AF_F32 ? bwd_group_split_f32(*a) : bwd_group_split(*a);
+  return AF_OK;
 }
 
 }  // extern "C"

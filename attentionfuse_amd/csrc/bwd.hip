@@ -10,7 +10,16 @@
 
 namespace af {
 
+// A caller's group_split must be a power of two dividing the group size.
+bool group_split_valid(const af_bwd_args& a) {
+  const int s = a.group_split;
+  if (s == 0) return true;
+  if (s < 0 || (s & (s - 1)) != 0 || a.heads_kv <= 0 || a.heads_q % a.heads_kv != 0) return false;
+  return (a.heads_q / a.heads_kv) % s == 0;
+}
+
 int bwd_group_split(const af_bwd_args& a) {
+  if (a.group_split > 0 && group_split_valid(a)) return a.group_split;
   if (a.batch <= 0 || a.heads_kv <= 0 || a.heads_q <= 0 || a.seqlen_kv <= 0 || a.heads_q % a.heads_kv != 0) return 1;
   const int G = a.heads_q / a.heads_kv;
   const int64_t base = (int64_t)((a.seqlen_kv + 127) / 128) * a.batch * a.heads_kv;
@@ -23,6 +32,7 @@ int bwd_group_split(const af_bwd_args& a) {
 // 4-wave workgroups per CU (256 CUs); causal key blocks differ in work by up
 // to N/128 times, so one workgroup per key block leaves most CUs idle at the end.
 int bwd_group_split_f32(const af_bwd_args& a) {
+  if (a.group_split > 0 && group_split_valid(a)) return a.group_split;
   if (a.batch <= 0 || a.heads_kv <= 0 || a.heads_q <= 0 || a.seqlen_kv <= 0 || a.heads_q % a.heads_kv != 0) return 1;
   const int G = a.heads_q / a.heads_kv;
   const int64_t base = (int64_t)((a.seqlen_kv + 127) / 128) * a.batch * a.heads_kv;
@@ -106,6 +116,8 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
     if (a->rope_len < std::max(a->seqlen_q, a->seqlen_kv)) return bad(AF_ERR_BAD_ARG, "rope tables too short");
   }
   if (k.bias == AF_BIAS_ALIBI && a->alibi_slopes == nullptr) return bad(AF_ERR_BAD_ARG, "ALiBi needs slopes");
+  if (!group_split_valid(*a))
+    return bad(AF_ERR_BAD_ARG, "group_split must be 0 or a power of two dividing heads_q / heads_kv");
   // the kernels stage Q, dO, K, V and the RoPE tables through buffer
   // resources with a 32-bit byte range per (batch, head) slice
   auto fits = [&](int64_t rows, int64_t stride) {

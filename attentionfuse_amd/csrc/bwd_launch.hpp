@@ -29,7 +29,10 @@ struct BwdWorkspace {
 // long key blocks do not leave most CUs idle.  Measured at config 5 (256
 // workgroups unsplit, one per CU): backward 1153 us unsplit, 796 us split 4
 // ways, 773 us split 2 ways; at B = 2 (512 workgroups) splitting lost.
+// The args' group_split when it is set, else the choice described above.
 int bwd_group_split(const af_bwd_args& a);
+bool group_split_valid(const af_bwd_args& a);
+int bwd_group_split_f32(const af_bwd_args& a);
 BwdWorkspace bwd_workspace_layout(const af_bwd_args& a);
 size_t bwd_workspace_bytes(const af_bwd_args& a);
 int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_t workspace_bytes,

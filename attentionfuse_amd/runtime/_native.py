@@ -87,7 +87,8 @@ class BwdArgsC(C.Structure):
                 ("batch", C.c_int32), ("heads_q", C.c_int32),
                 ("heads_kv", C.c_int32), ("seqlen_q", C.c_int32),
                 ("seqlen_kv", C.c_int32), ("rope_len", C.c_int32),
-                ("scale", C.c_float), ("window", C.c_int32)]
+                ("scale", C.c_float), ("window", C.c_int32),
+                ("group_split", C.c_int32)]
 
 
 # Every symbol the header declares, with its ctypes signature.
@@ -106,6 +107,9 @@ SIGNATURES = {
     "af_bwd_workspace_bytes": (C.c_size_t, [C.POINTER(BwdArgsC)]),
     "af_bwd": (C.c_int, [C.POINTER(BwdArgsC), C.POINTER(BlockMaskC),
                          C.c_void_p, C.c_size_t, C.c_void_p]),
+    "af_bwd_tile": (C.c_int, [C.POINTER(BwdArgsC), C.POINTER(BlockMaskC),
+                              C.POINTER(C.c_int32), C.POINTER(C.c_int32),
+                              C.POINTER(C.c_int32)]),
     "af_query": (C.c_int, [C.POINTER(SpecKeyC)]),
     "af_fwd_tile": (C.c_int, [C.POINTER(SpecKeyC), C.POINTER(C.c_int32),
                               C.POINTER(C.c_int32)]),
@@ -113,7 +117,7 @@ SIGNATURES = {
     "af_abi_version": (C.c_int, []),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib = None
 _lock = threading.Lock()

@@ -30,6 +30,37 @@ def can_backward(graph: Graph) -> bool:
     return True
 
 
+# Backward launch override, the counterpart of the reference's _BWD_TILE
+# (reference: attnfuse/runtime/backward.py:18-47).  On gfx950 the block
+# shapes are fixed per instantiation (128-row dQ and 128-key dK/dV
+# workgroups, or the BlockMask's blocks); the runtime choice is how many
+# dK/dV workgroups split one key block's GQA query heads.  With "auto" the
+# library picks it (``_pick_backward_tile``); otherwise "group_split" (a
+# power of two dividing H_q / H_kv) is used as given, e.g.
+#     backward._BWD_TILE.update({"auto": False, "group_split": 2})
+_BWD_TILE = {
+    "group_split": 0,
+    "auto": True,
+}
+
+
+def _group_split_request() -> int:
+    if _BWD_TILE.get("auto", True):
+        return 0
+    return int(_BWD_TILE.get("group_split", 0) or 0)
+
+
+def _pick_backward_tile(args: "N.BwdArgsC", block_mask=None) -> dict:
+    """The backward launch shape for these packed arguments, as the library
+    will use it: {"BLOCK_M", "BLOCK_N", "group_split"}."""
+    import ctypes as C
+    bm, bn, gs = C.c_int32(), C.c_int32(), C.c_int32()
+    c_bm = block_mask._c() if block_mask is not None else None
+    N.check(N.lib().af_bwd_tile(args, c_bm, C.byref(bm), C.byref(bn),
+                                C.byref(gs)))
+    return {"BLOCK_M": bm.value, "BLOCK_N": bn.value, "group_split": gs.value}
+
+
 def _bwd_workspace(device, nbytes: int) -> torch.Tensor:
     return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
 
@@ -73,6 +104,7 @@ def _run_backward_key(key, Q, K, V, O, L, dO, sm_scale, window, cos, sin,
     a.rope_len = 0 if c is None else c.shape[0]
     a.scale = float(sm_scale)
     a.window = int(window or 0)
+    a.group_split = _group_split_request()
     nbytes = int(N.lib().af_bwd_workspace_bytes(a))
     ws = _bwd_workspace(Q.device, nbytes)
     bm = block_mask._c() if block_mask is not None else None

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define AF_ABI_VERSION 3
+#define AF_ABI_VERSION 4
 
 typedef enum af_status {
   AF_OK = 0,
@@ -197,6 +197,11 @@ typedef struct af_bwd_args {
   int32_t batch, heads_q, heads_kv, seqlen_q, seqlen_kv, rope_len;
   float scale;
   int32_t window;
+  int32_t group_split; /* dK/dV workgroups sharing one key block's GQA query
+                          heads: 0 = library default (af_bwd_tile), else a
+                          power of two dividing heads_q / heads_kv.  Replaces
+                          the reference's _BWD_TILE override
+                          (attnfuse/runtime/backward.py:26-47). */
 } af_bwd_args;
 
 /* Workspace bytes af_bwd needs for these arguments: the log2-scaled LSE and
@@ -209,6 +214,15 @@ size_t af_bwd_workspace_bytes(const af_bwd_args* args);
  * and windowed masks only, bm must then be NULL). */
 int af_bwd(const af_bwd_args* args, const af_blockmask* bm /* nullable */,
            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward launch shape for these arguments: query rows per dQ workgroup,
+ * keys per dK/dV workgroup and the GQA group split the launch uses (the
+ * args' group_split, or the library's choice when it is 0).  With a block
+ * mask (nullable) the block sizes are the mask's.  Any output pointer may be
+ * NULL.  Replaces the reference's _pick_backward_tile
+ * (attnfuse/runtime/backward.py:35-47). */
+int af_bwd_tile(const af_bwd_args* args, const af_blockmask* bm,
+                int32_t* block_m, int32_t* block_n, int32_t* group_split);
 
 /* 1 if an instantiation exists for the key (forward; decode and backward
  * accept the subsets documented above), else 0. */

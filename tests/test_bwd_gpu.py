@@ -174,3 +174,19 @@ def test_explicit_alibi_slopes_reach_the_backward():
                                           causal=True, alibi_slopes=slopes)
     check({"O": (out.detach().float().cpu() - o_ref).abs().max().item(),
            "dQ": rel(q.grad, dq), "dK": rel(k.grad, dk), "dV": rel(v.grad, dv)}, dtype)
+
+
+@pytest.mark.parametrize("split", [1, 2, 4])
+def test_backward_group_split_override(split):
+    """_BWD_TILE's group split reaches the launch: every split of config 5's
+    GQA group of 4 (the library picks 4 at N=512) gives oracle-exact
+    gradients."""
+    from attentionfuse_amd.runtime import backward as bwd
+    print(f"[bwd] group_split={split}", flush=True)
+    saved = dict(bwd._BWD_TILE)
+    try:
+        bwd._BWD_TILE.update({"auto": False, "group_split": split})
+        check(run("rope_causal", 1, 8, 2, 512, 128, torch.bfloat16, base=500000.0), torch.bfloat16)
+    finally:
+        bwd._BWD_TILE.clear()
+        bwd._BWD_TILE.update(saved)

@@ -15,13 +15,13 @@ from attnfuse.ir.high_level import (BiasKind, Graph, MaskKind, MatMulPV,
 from attnfuse.ir.printer import format_graph, format_tiled
 
 
-def _zeros(D=32, N=16, H=2):
-    z = torch.zeros(1, H, N, D)
+def _zeros(D=32, N=16, H=2, dtype=torch.float32):
+    z = torch.zeros(1, H, N, D, dtype=dtype)
     return z, z.clone(), z.clone()
 
 
-def _trace(fn, D=64, H=4, N=16):
-    return fn(*_zeros(D, N, H), return_graph=True)
+def _trace(fn, D=64, H=4, N=16, dtype=torch.float32):
+    return fn(*_zeros(D, N, H, dtype), return_graph=True)
 
 
 def test_import_and_version():
@@ -189,13 +189,99 @@ def test_fusion_checks():
 
 
 def test_tile_config_for_each_head_dim():
+    """A tile for every instantiated head dim (the reference's
+    tests/test_compiler.py:25-32 loop); a head dim with no kernels raises
+    NotImplementedError instead of returning a table entry that no launch
+    uses."""
+    from attentionfuse_amd.compiler.tiling import SUPPORTED_HEAD_DIMS
     for D in (32, 64, 96, 128, 256):
         @af.attention
         def fn(Q, K, V):
             return af.softmax(af.scaled_dot_product(Q, K)) @ V
+        if D not in SUPPORTED_HEAD_DIMS:
+            with pytest.raises(NotImplementedError):
+                choose_tile_config(_trace(fn, D=D))
+            continue
         cfg = choose_tile_config(_trace(fn, D=D))
         assert cfg.BLOCK_M >= 32 and cfg.BLOCK_N >= 16
         assert cfg.BLOCK_M == 32 * cfg.waves
+
+
+def test_key_config_is_the_librarys_tile_for_every_instantiated_key():
+    """lower_to_key(...).config is what af_fwd_tile reports, for every
+    (dtype, head dim, mask, bias, norm, rope) the library instantiates."""
+    import ctypes as C
+    import itertools
+
+    from attentionfuse_amd.compiler.tiling import SUPPORTED_HEAD_DIMS, tile_for_key
+    from attentionfuse_amd.runtime import _native as N
+    lib = N.lib()
+    variants = {
+        "dense": lambda Q, K, V: af.softmax(af.scaled_dot_product(Q, K)) @ V,
+        "causal": lambda Q, K, V: af.softmax(af.causal(af.scaled_dot_product(Q, K))) @ V,
+        "sw": lambda Q, K, V: af.softmax(af.sliding_window(af.scaled_dot_product(Q, K), 64)) @ V,
+        "csw": lambda Q, K, V: af.softmax(af.causal(af.sliding_window(af.scaled_dot_product(Q, K), 64))) @ V,
+        "bs": lambda Q, K, V: af.softmax(af.block_sparse(af.scaled_dot_product(Q, K))) @ V,
+        "alibi": lambda Q, K, V: af.softmax(af.causal(af.alibi(af.scaled_dot_product(Q, K), 4))) @ V,
+        "add": lambda Q, K, V: af.softmax(af.additive_bias(af.scaled_dot_product(Q, K))) @ V,
+        "relu": lambda Q, K, V: af.relu_attention(af.causal(af.scaled_dot_product(Q, K))) @ V,
+        "rope": lambda Q, K, V: af.softmax(af.causal(af.rope(Q, K))) @ V,
+    }
+    checked = 0
+    for dt, D, (name, fn) in itertools.product(
+            (torch.float16, torch.bfloat16, torch.float32), SUPPORTED_HEAD_DIMS, variants.items()):
+        g = _trace(af.attention(fn), D=D, dtype=dt)
+        try:
+            k = lower_to_tiled(g)
+        except NotImplementedError:
+            # lowering refuses exactly the keys the library does not have
+            from attnfuse.ir.spec import DTYPE_CODES
+            codes = {"dense": (0, 0, 0, 0), "causal": (1, 0, 0, 0), "sw": (2, 0, 0, 0), "csw": (4, 0, 0, 0),
+                     "bs": (3, 0, 0, 0), "alibi": (1, 1, 0, 0), "add": (0, 2, 0, 0), "relu": (1, 0, 1, 0),
+                     "rope": (1, 0, 0, 1)}[name]
+            assert not lib.af_query(N.SpecKeyC(DTYPE_CODES[str(dt).replace("torch.", "")], D, *codes))
+            continue
+        assert lib.af_query(N.SpecKeyC(*k.abi_tuple()))
+        bm, bn = C.c_int32(), C.c_int32()
+        assert lib.af_fwd_tile(N.SpecKeyC(*k.abi_tuple()), C.byref(bm), C.byref(bn)) == 0
+        assert (k.config.BLOCK_M, k.config.BLOCK_N) == (bm.value, bn.value), (name, dt, D)
+        assert k.config.waves == bm.value // 32
+        checked += 1
+    assert checked >= 2 * 3 * 9 + 3 * 8
+    # every key the library accepts, not only those a graph lowers to
+    for key in itertools.product((0, 1, 2), SUPPORTED_HEAD_DIMS, range(5), range(3), range(2), range(2)):
+        if lib.af_query(N.SpecKeyC(*key)):
+            cfg = tile_for_key(key)
+            assert cfg.BLOCK_M % 32 == 0 and cfg.BLOCK_N in (32, 64)
+
+
+def test_backward_tile_override_reaches_the_library():
+    """_BWD_TILE / _pick_backward_tile: the library's default group split,
+    an explicit power-of-two override, and the refusal of a bad one."""
+    from attentionfuse_amd.runtime import _native as N
+    from attentionfuse_amd.runtime import backward as bwd
+    a = N.BwdArgsC()
+    a.key = N.SpecKeyC(1, 128, 1, 0, 0, 1)
+    a.batch, a.heads_q, a.heads_kv, a.seqlen_q, a.seqlen_kv = 1, 32, 8, 4096, 4096
+    auto = bwd._pick_backward_tile(a)
+    assert (auto["BLOCK_M"], auto["BLOCK_N"]) == (128, 128)
+    assert auto["group_split"] in (1, 2, 4)
+    a.group_split = 4
+    assert bwd._pick_backward_tile(a)["group_split"] == 4
+    a.group_split = 3
+    with pytest.raises(ValueError):
+        bwd._pick_backward_tile(a)
+    a.group_split = 8                       # does not divide the group of 4
+    with pytest.raises(ValueError):
+        bwd._pick_backward_tile(a)
+    saved = dict(bwd._BWD_TILE)
+    try:
+        bwd._BWD_TILE.update({"auto": False, "group_split": 2})
+        assert bwd._group_split_request() == 2
+    finally:
+        bwd._BWD_TILE.clear()
+        bwd._BWD_TILE.update(saved)
+    assert bwd._group_split_request() == 0
 
 
 def test_constexprs_change_with_variant():
