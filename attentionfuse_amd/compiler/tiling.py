@@ -21,7 +21,7 @@ from ..ir.high_level import Graph
 from ..ir.spec import TileConfig
 
 # Head dims with kernels in libattnfuse_hip.so (af_query accepts them).
-SUPPORTED_HEAD_DIMS = (32, 64, 128)
+SUPPORTED_HEAD_DIMS = (32, 64, 128, 256)
 LDS_STAGES = 2
 
 

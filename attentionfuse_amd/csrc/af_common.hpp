@@ -343,7 +343,7 @@ __device__ __forceinline__ uint32_t span_bytes(int rows, int64_t rstride) {
 // ---------------------------------------------------------------------------
 template <int D>
 __device__ __forceinline__ int lds_swz(int r) {
-  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  if constexpr (D >= 128) return ((r & 3) << 2) | ((r >> 2) & 3);
   else if constexpr (D == 64) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
   else return (r >> 2) & 3;
 }

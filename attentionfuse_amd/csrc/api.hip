@@ -51,8 +51,10 @@ int check_key(const af_spec_key& k, bool allow_bs, bool allow_f32 = false) {
   } else if (k.dtype != AF_F16 && k.dtype != AF_BF16) {
     return fail(AF_ERR_UNSUPPORTED, "dtype %d: the gfx950 kernels take fp16, bf16 or (forward) fp32", k.dtype);
   }
-  if (k.head_dim != 32 && k.head_dim != 64 && k.head_dim != 128)
-    return fail(AF_ERR_UNSUPPORTED, "head_dim %d: instantiated for 32, 64 and 128", k.head_dim);
+  if (k.head_dim != 32 && k.head_dim != 64 && k.head_dim != 128 && k.head_dim != 256)
+    return fail(AF_ERR_UNSUPPORTED, "head_dim %d: instantiated for 32, 64, 128 and 256", k.head_dim);
+  if (k.head_dim == 256 && k.dtype == AF_F32)
+    return fail(AF_ERR_UNSUPPORTED, "head_dim 256: the fp32 kernels take head dims 32, 64 and 128");
   if (k.mask < 0 || k.mask > 4 || (!allow_bs && k.mask == AF_MASK_BLOCK_SPARSE))
     return fail(AF_ERR_UNSUPPORTED, "mask kind %d not valid here", k.mask);
   if (k.bias < 0 || k.bias > 2) return fail(AF_ERR_UNSUPPORTED, "bias kind %d", k.bias);
@@ -173,6 +175,7 @@ int rotate_keys(FwdParams& p, const af_fwd_args& a, void* workspace, size_t work
     case 32: f16 ? launch_rope_f16_d32(r, s) : launch_rope_bf16_d32(r, s); break;
     case 64: f16 ? launch_rope_f16_d64(r, s) : launch_rope_bf16_d64(r, s); break;
     case 128: f16 ? launch_rope_f16_d128(r, s) : launch_rope_bf16_d128(r, s); break;
+    case 256: f16 ? launch_rope_f16_d256(r, s) : launch_rope_bf16_d256(r, s); break;
   }
   p.k = r.out;
   p.ks[3] = 1;
@@ -211,6 +214,10 @@ int dispatch_fwd(FwdParams p, const af_fwd_args& a, int waves, void* workspace, 
     case 128:
       rc = f16 ? launch_fwd_f16_d128(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s)
                : launch_fwd_bf16_d128(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s);
+      break;
+    case 256:
+      rc = f16 ? launch_fwd_f16_d256(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s)
+               : launch_fwd_bf16_d256(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s);
       break;
   }
   if (rc != 0) return fail(AF_ERR_UNSUPPORTED, "no forward instantiation for this key");

@@ -4,7 +4,8 @@ Usage: python -m attentionfuse_amd.csrc.build [--jobs N] [--quick]
 
 Every HIP source is compiled with -Xclang -target-feature -Xclang
 -packed-fp32-ops (packed fp32 VALU instructions are kept out of the code
-objects) and linked into attentionfuse_amd/libattnfuse_hip.so.
+objects) and linked into attentionfuse_amd/libattnfuse_hip.so.  All but the
+units in DEFAULT_FORM_UNITS keep MFMA accumulators in VGPRs.
 """
 from __future__ import annotations
 
@@ -25,14 +26,16 @@ BUILD = ROOT / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-FLAGS = [
+BASE_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # keep MFMA accumulators in VGPRs: VALU work on them (the softmax
-    # rescale) then needs no AGPR<->VGPR copies around the loop
-    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     f"-I{ROOT / 'include'}", f"-I{HERE}", "-Wno-unused-result",
 ]
+# keep MFMA accumulators in VGPRs: VALU work on them (the softmax rescale)
+# then needs no AGPR<->VGPR copies around the loop
+FLAGS = BASE_FLAGS + ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+# units built with the compiler's default MFMA register form
+DEFAULT_FORM_UNITS = {"fwd_d256_alt", "bwd_d256_alt"}
 
 # (object name, source, extra defines)
 UNITS = [
@@ -42,17 +45,24 @@ UNITS = [
     ("bwd", "bwd.hip", []),
     ("fwd_f32", "fwd_f32.hip", []),
     ("bwd_f32", "bwd_f32.hip", []),
+    ("fwd_d256_alt", "fwd_d256_alt.hip", []),
+    ("bwd_d256_alt", "bwd_d256_alt.hip", []),
 ] + [
     (f"{kind}_{dt}_d{d}", f"{kind}_inst.hip", [f"-DAF_DT={code}", f"-DAF_D={d}"])
     for kind in ("fwd", "bwd")
     for dt, code in (("f16", 0), ("bf16", 1)) for d in (32, 64, 128)
+] + [
+    # head dim 256: one wave per SIMD, accumulators past 256 registers in AGPRs
+    (f"{kind}_{dt}_d256", f"{kind}_inst.hip", [f"-DAF_DT={code}", "-DAF_D=256"])
+    for kind in ("fwd", "bwd") for dt, code in (("f16", 0), ("bf16", 1))
 ]
 
 
 def _compile(unit) -> tuple:
     name, src, defs = unit
     obj = BUILD / f"{name}.o"
-    cmd = [HIPCC, *FLAGS, *defs, "-c", str(HERE / src), "-o", str(obj)]
+    flags = BASE_FLAGS if name in DEFAULT_FORM_UNITS else FLAGS
+    cmd = [HIPCC, *flags, *defs, "-c", str(HERE / src), "-o", str(obj)]
     t0 = time.time()
     r = subprocess.run(cmd, capture_output=True, text=True)
     errs = "\n".join(l for l in r.stderr.splitlines()

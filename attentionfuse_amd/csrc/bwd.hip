@@ -84,7 +84,8 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
     return bad(AF_ERR_UNSUPPORTED, "backward takes fp16, bf16 or fp32");
   if (f32 && k.mask == AF_MASK_BLOCK_SPARSE)
     return bad(AF_ERR_UNSUPPORTED, "the block-sparse backward takes fp16 or bf16");
-  if (!head_dim_supported(k.head_dim)) return bad(AF_ERR_UNSUPPORTED, "backward head_dim must be 32, 64 or 128");
+  if (!head_dim_supported(k.head_dim)) return bad(AF_ERR_UNSUPPORTED, "backward head_dim must be 32, 64, 128 or 256");
+  if (f32 && k.head_dim == 256) return bad(AF_ERR_UNSUPPORTED, "the fp32 backward takes head dims 32, 64 and 128");
   if (k.mask < 0 || k.mask > 4) return bad(AF_ERR_UNSUPPORTED, "unknown mask kind");
   if (k.bias != AF_BIAS_NONE && k.bias != AF_BIAS_ALIBI)
     return bad(AF_ERR_UNSUPPORTED, "backward supports no bias or ALiBi");
@@ -265,6 +266,10 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
     case 128:
       r = f16 ? launch_bwd_f16_d128(p, k.mask, k.bias, k.rope, g, stream)
               : launch_bwd_bf16_d128(p, k.mask, k.bias, k.rope, g, stream);
+      break;
+    case 256:
+      r = f16 ? launch_bwd_f16_d256(p, k.mask, k.bias, k.rope, g, stream)
+              : launch_bwd_bf16_d256(p, k.mask, k.bias, k.rope, g, stream);
       break;
   }
   if (r != 0) return bad(AF_ERR_UNSUPPORTED, "no backward instantiation for this key");

@@ -38,14 +38,22 @@ size_t bwd_workspace_bytes(const af_bwd_args& a);
 int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_t workspace_bytes,
             hipStream_t stream);
 
+// dK/dV with ALiBi at head dim 256 (any dtype code 0/1, mask, rope, 2 or 4
+// waves), built in bwd_d256_alt.hip with the compiler's default MFMA
+// register form.  Returns -1 for a combination it does not hold.
+int launch_bwd_dkv_d256_alibi(const BwdParams& p, int dtype, int mask, bool rope, int waves, dim3 grid,
+                              hipStream_t s);
+
 #define AF_DECLARE_BWD(NAME) \
   int NAME(const BwdParams& p, int mask, int bias, int rope, const BwdGrids& g, hipStream_t s);
 AF_DECLARE_BWD(launch_bwd_f16_d32)
 AF_DECLARE_BWD(launch_bwd_f16_d64)
 AF_DECLARE_BWD(launch_bwd_f16_d128)
+AF_DECLARE_BWD(launch_bwd_f16_d256)
 AF_DECLARE_BWD(launch_bwd_bf16_d32)
 AF_DECLARE_BWD(launch_bwd_bf16_d64)
 AF_DECLARE_BWD(launch_bwd_bf16_d128)
+AF_DECLARE_BWD(launch_bwd_bf16_d256)
 #undef AF_DECLARE_BWD
 
 }  // namespace af

@@ -23,6 +23,7 @@ int pick_d(const DecodeParams& p, int d, int bias, dim3 gs, dim3 gc, hipStream_t
     case 32: return pick_bias<E, 32>(p, bias, gs, gc, s);
     case 64: return pick_bias<E, 64>(p, bias, gs, gc, s);
     case 128: return pick_bias<E, 128>(p, bias, gs, gc, s);
+    case 256: return pick_bias<E, 256>(p, bias, gs, gc, s);
     default: return -1;
   }
 }

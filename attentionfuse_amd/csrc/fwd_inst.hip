@@ -25,10 +25,22 @@ using Elem = BF16;
 
 namespace {
 
+// bf16, head dim 256, causal + additive bias + ReLU + RoPE crashes the
+// compiler's backend when MFMAs are forced into the VGPR form; that one
+// kernel is built in fwd_d256_alt.hip without the flag.
+constexpr bool alt_unit(int mask, int bias, int norm, bool rope, int waves) {
+  return AF_DT == 1 && AF_D == 256 && mask == MASK_CAUSAL && bias == BIAS_ADD && norm == NORM_RELU && rope &&
+         waves == 4;
+}
+
 template <int MASK, int BIAS, int NORM, bool ROPE, int WAVES>
 int go(const FwdParams& p, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((fwd_kernel<Elem, AF_D, MASK, BIAS, NORM, ROPE, WAVES>),
-                     grid, dim3(64 * WAVES), 0, s, p);
+  if constexpr (alt_unit(MASK, BIAS, NORM, ROPE, WAVES)) {
+    launch_fwd_bf16_d256_causal_add_relu_rope(p, grid, s);
+  } else {
+    hipLaunchKernelGGL((fwd_kernel<Elem, AF_D, MASK, BIAS, NORM, ROPE, WAVES>),
+                       grid, dim3(64 * WAVES), 0, s, p);
+  }
   return 0;
 }
 

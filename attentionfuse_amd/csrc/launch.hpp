@@ -23,19 +23,27 @@ void set_error(const char* fmt, ...);
 AF_DECLARE_FWD(launch_fwd_f16_d32)
 AF_DECLARE_FWD(launch_fwd_f16_d64)
 AF_DECLARE_FWD(launch_fwd_f16_d128)
+AF_DECLARE_FWD(launch_fwd_f16_d256)
 AF_DECLARE_FWD(launch_fwd_bf16_d32)
 AF_DECLARE_FWD(launch_fwd_bf16_d64)
 AF_DECLARE_FWD(launch_fwd_bf16_d128)
+AF_DECLARE_FWD(launch_fwd_bf16_d256)
 #undef AF_DECLARE_FWD
+
+// bf16, head dim 256, causal + additive bias + ReLU + RoPE, built in
+// fwd_d256_alt.hip with the compiler's default MFMA register form.
+void launch_fwd_bf16_d256_causal_add_relu_rope(const FwdParams& p, dim3 grid, hipStream_t stream);
 
 // rope_rows_kernel launchers, defined next to the forward launchers.
 #define AF_DECLARE_ROPE(NAME) int NAME(const RopeRowsParams& p, hipStream_t stream);
 AF_DECLARE_ROPE(launch_rope_f16_d32)
 AF_DECLARE_ROPE(launch_rope_f16_d64)
 AF_DECLARE_ROPE(launch_rope_f16_d128)
+AF_DECLARE_ROPE(launch_rope_f16_d256)
 AF_DECLARE_ROPE(launch_rope_bf16_d32)
 AF_DECLARE_ROPE(launch_rope_bf16_d64)
 AF_DECLARE_ROPE(launch_rope_bf16_d128)
+AF_DECLARE_ROPE(launch_rope_bf16_d256)
 #undef AF_DECLARE_ROPE
 
 // fp32 forward and fp32 key rotation, defined in fwd_f32.hip; return -1 for

@@ -35,6 +35,6 @@ inline int check_bhnd(const char* name, const void* ptr, const int64_t* st, int6
   return AF_OK;
 }
 
-inline bool head_dim_supported(int d) { return d == 32 || d == 64 || d == 128; }
+inline bool head_dim_supported(int d) { return d == 32 || d == 64 || d == 128 || d == 256; }
 
 }  // namespace af

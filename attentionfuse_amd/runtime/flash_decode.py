@@ -32,7 +32,7 @@ def can_use_flash_decode(graph: Graph, Q: torch.Tensor, K: torch.Tensor) -> bool
         return False
     if graph.has_rope or graph.norm().kind is not NormKind.SOFTMAX:
         return False
-    return Q.shape[-1] in (32, 64, 128) and Q.dtype in (torch.float16,
+    return Q.shape[-1] in (32, 64, 128, 256) and Q.dtype in (torch.float16,
                                                          torch.bfloat16)
 
 

@@ -67,7 +67,7 @@ typedef enum af_norm { AF_NORM_SOFTMAX = 0, AF_NORM_RELU = 1 } af_norm;
  * (attnfuse/compiler/codegen.py:391-404; attnfuse/ir/tiled.py:52-81). */
 typedef struct af_spec_key {
   int32_t dtype;     /* af_dtype; AF_F32: af_fwd and af_bwd, not block-sparse or decode */
-  int32_t head_dim;  /* instantiated: 32, 64, 128 (af_query) */
+  int32_t head_dim;  /* instantiated: 32, 64, 128, 256 (256: fp16/bf16 only; af_query) */
   int32_t mask;      /* af_mask                   */
   int32_t bias;      /* af_bias                   */
   int32_t norm;      /* af_norm                   */

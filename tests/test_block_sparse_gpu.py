@@ -155,3 +155,21 @@ def test_rope_and_alibi_with_block_mask():
     assert (out.detach().float().cpu() - o_ref).abs().max().item() <= TOL[torch.float16]
     for got, ref in ((q.grad, dq), (k.grad, dk), (v.grad, dv)):
         assert ((got.float().cpu() - ref).norm() / ref.norm()).item() <= GRAD_REL
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_head_dim_256_forward_and_backward(dtype):
+    """BigBird-style block mask at head dim 256, forward and backward."""
+    print(f"[bs] D256 {dtype}", flush=True)
+    Q, K, V, dO = make(1, 2, N, 256, dtype, seed=3)
+    bm = af.create_block_mask(PATTERNS["bigbird"], N, N, 64, 64)
+    q, k, v = (t.clone().requires_grad_(True) for t in (Q, K, V))
+    out = bs_attn(q, k, v, block_mask=bm)
+    out.backward(dO)
+    torch.cuda.synchronize()
+    grid = O.block_grid(PATTERNS["bigbird"], N, N, 64, 64)
+    o_ref, dq, dk, dv = O.attention_grads(Q.cpu(), K.cpu(), V.cpu(), dO.cpu(), dtype=torch.float32,
+                                          elem_mask=elem_mask(grid, N))
+    assert (out.detach().float().cpu() - o_ref).abs().max().item() <= TOL[dtype]
+    for got, ref in ((q.grad, dq), (k.grad, dk), (v.grad, dv)):
+        assert ((got.float().cpu() - ref).norm() / ref.norm()).item() <= GRAD_REL

@@ -190,3 +190,12 @@ def test_backward_group_split_override(split):
     finally:
         bwd._BWD_TILE.clear()
         bwd._BWD_TILE.update(saved)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("name", ["causal", "rope_causal", "rope_causal_alibi", "dense", "alibi", "sw"])
+def test_backward_head_dim_256(name, dtype):
+    """Head dim 256 with a GQA group of 2 (the ALiBi dK/dV kernels come from
+    their own unit, bwd_d256_alt.hip)."""
+    print(f"[bwd] D256 {name} {dtype}", flush=True)
+    check(run(name, 1, 4, 2, 192, 256, dtype), dtype)

@@ -32,7 +32,8 @@ def alibi_fn(H):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
 @pytest.mark.parametrize("shape", [(2, 8, 2, 4096, 128), (1, 32, 8, 2048, 128), (2, 4, 4, 1000, 64),
-                                   (1, 16, 1, 3000, 64), (1, 32, 1, 777, 128), (3, 6, 3, 513, 32)])
+                                   (1, 16, 1, 3000, 64), (1, 32, 1, 777, 128), (3, 6, 3, 513, 32),
+                                   (2, 8, 4, 3000, 256), (1, 16, 8, 8192, 256)])
 def test_decode_matches_oracle(shape, dtype):
     B, Hq, Hkv, N, D = shape
     print(f"[decode] {shape} {dtype}", flush=True)

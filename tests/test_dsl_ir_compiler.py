@@ -200,9 +200,9 @@ def test_tile_config_for_each_head_dim():
             return af.softmax(af.scaled_dot_product(Q, K)) @ V
         if D not in SUPPORTED_HEAD_DIMS:
             with pytest.raises(NotImplementedError):
-                choose_tile_config(_trace(fn, D=D))
+                choose_tile_config(_trace(fn, D=D, dtype=torch.float16))
             continue
-        cfg = choose_tile_config(_trace(fn, D=D))
+        cfg = choose_tile_config(_trace(fn, D=D, dtype=torch.float16))
         assert cfg.BLOCK_M >= 32 and cfg.BLOCK_N >= 16
         assert cfg.BLOCK_M == 32 * cfg.waves
 

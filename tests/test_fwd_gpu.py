@@ -117,6 +117,35 @@ def test_head_dims(name, D, dtype):
     assert err <= TOL[dtype], f"{name} D={D}: max|err|={err:.3e}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("name", ["dense", "causal", "rope_causal", "rope_causal_alibi", "sw", "sw_causal",
+                                  "additive", "relu_causal", "alibi"])
+def test_head_dim_256(name, dtype):
+    """Head dim 256 (Gemma-class models; the reference's tile tables carry
+    it, attnfuse/compiler/tiling.py:29-60): every variant, a GQA ratio and a
+    ragged length."""
+    print(f"[fwd] D256 {name} {dtype}", flush=True)
+    err = run_case(name, 1, 4, 2, 200, 256, dtype)
+    assert err <= TOL[dtype], f"{name} D=256: max|err|={err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_head_dim_256_relu_additive_rope(dtype):
+    """causal + additive bias + ReLU + RoPE at head dim 256: the bf16 kernel
+    is built in its own unit (fwd_d256_alt.hip)."""
+    fn = lambda Q, K, V: af.relu_attention(af.causal(af.additive_bias(af.rope(Q, K)))) @ V  # noqa: E731
+    B, H, N, D = 1, 2, 160, 256
+    Q, K, V = make(B, H, H, N, N, D, dtype, seed=8)
+    g = torch.Generator(device="cuda").manual_seed(9)
+    bias = torch.randn(B, H, N, N, generator=g, device="cuda", dtype=dtype)
+    cos, sin = build_rope_cache(N, D, device="cuda", dtype=dtype)
+    out = af.attention(fn)(Q, K, V, bias=bias, cos=cos, sin=sin)
+    torch.cuda.synchronize()
+    want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(), causal=True, norm="relu", bias=bias.cpu(),
+                             rope=(cos[0, 0].cpu(), sin[0, 0].cpu()))
+    assert (out.float().cpu() - want).abs().max().item() <= TOL[dtype]
+
+
 @pytest.mark.parametrize("N", [1, 17, 64, 200, 333])
 @pytest.mark.parametrize("name", ["causal", "rope_causal", "sw", "dense", "additive"])
 def test_ragged_lengths(name, N):
