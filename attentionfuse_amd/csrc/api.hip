@@ -38,16 +38,14 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-// allow_f32: the entry point has an fp32 kernel (the dense / causal /
-// windowed forward; af_bwd checks its own keys; decode and block-sparse
-// have none).
+// allow_f32: the entry point has fp32 kernels (the forward, block-sparse
+// included, and decode; af_bwd checks its own keys).
 int check_key(const af_spec_key& k, bool allow_bs, bool allow_f32 = false) {
   if (k.dtype == AF_F32) {
     if (!allow_f32)
       return fail(AF_ERR_UNSUPPORTED, "dtype fp32: af_fwd and af_bwd take fp32 (dense / causal / windowed masks); "
                   "this entry point takes fp16 or bf16");
-    if (k.mask == AF_MASK_BLOCK_SPARSE)
-      return fail(AF_ERR_UNSUPPORTED, "dtype fp32: the block-sparse kernels take fp16 or bf16");
+
   } else if (k.dtype != AF_F16 && k.dtype != AF_BF16) {
     return fail(AF_ERR_UNSUPPORTED, "dtype %d: the gfx950 kernels take fp16, bf16 or (forward) fp32", k.dtype);
   }
@@ -228,11 +226,23 @@ int dispatch_fwd(FwdParams p, const af_fwd_args& a, int waves, void* workspace, 
 
 // fp32 forward: keys rotated once into the workspace with RoPE, then
 // fwd_f32_kernel over 128-row query blocks.
-int dispatch_fwd_f32(const af_fwd_args& a, void* workspace, size_t workspace_bytes, hipStream_t s) {
+int dispatch_fwd_f32(const af_fwd_args& a, void* workspace, size_t workspace_bytes, hipStream_t s,
+                     const af_blockmask* bm = nullptr) {
   if (a.coverage != nullptr)
     return fail(AF_ERR_UNSUPPORTED, "tile-visit counters are kept by the fp16/bf16 kernels only");
   FwdF32Params fp;
   fp.f = make_fwd_params(&a, kF32BlockM);
+  if (bm != nullptr) {
+    FwdParams& q = fp.f;
+    q.bs_block_m = bm->block_m;
+    q.bs_block_n = bm->block_n;
+    q.bs_full_num = bm->full_kv_num;
+    q.bs_full_idx = bm->full_kv_idx;
+    q.bs_part_num = bm->kv_num_blocks;
+    q.bs_part_idx = bm->kv_indices;
+    q.bs_full_rs = bm->full_kv_stride;
+    q.bs_part_rs = bm->kv_stride;
+  }
   fp.mask = a.key.mask;
   fp.bias = a.key.bias;
   fp.norm = a.key.norm;
@@ -277,7 +287,7 @@ int plan_decode(const af_decode_args* a, size_t max_ws, DecodeParams* out, size_
   if ((rc = check_bhnd("v", a->v, a->v_stride, a->seqlen_kv))) return rc;
   if (a->o == nullptr) return fail(AF_ERR_BAD_ARG, "o is NULL");
   if (a->o_stride[3] != 1) return fail(AF_ERR_BAD_ARG, "o: head-dim stride must be 1");
-  if ((rc = check_key(a->key, false))) return rc;
+  if ((rc = check_key(a->key, false, true))) return rc;
   if (a->key.mask != AF_MASK_FULL || a->key.rope != 0 || a->key.norm != AF_NORM_SOFTMAX ||
       (a->key.bias != AF_BIAS_NONE && a->key.bias != AF_BIAS_ALIBI))
     return fail(AF_ERR_UNSUPPORTED, "decode takes dense softmax with no bias or ALiBi, no RoPE");
@@ -324,7 +334,10 @@ int plan_decode(const af_decode_args* a, size_t max_ws, DecodeParams* out, size_
   p.Hkv = a->heads_kv;
   p.Nkv = a->seqlen_kv;
   p.G = a->heads_q / a->heads_kv;
-  p.nqc = (p.G + 15) / 16;
+  // query heads sharing one workgroup's K/V reads: 16 (16-bit MFMA kernel)
+  // or f32_decode_heads(D) (fp32 VALU kernel)
+  const int gq = a->key.dtype == AF_F32 ? f32_decode_heads(D) : 16;
+  p.nqc = (p.G + gq - 1) / gq;
   p.nsplit = S;
   p.split_len = split_len;
   p.scale = a->scale;
@@ -393,22 +406,31 @@ int af_fwd_blocksparse(const af_fwd_args* a, const af_blockmask* bm, void* works
                        void* stream) {
   int rc = check_fwd_common(a);
   if (rc) return rc;
-  if ((rc = check_key(a->key, true))) return rc;
+  if ((rc = check_key(a->key, true, true))) return rc;
   if (a->key.mask != AF_MASK_BLOCK_SPARSE)
     return fail(AF_ERR_BAD_ARG, "af_fwd_blocksparse needs key.mask == AF_MASK_BLOCK_SPARSE");
+  const bool f32 = a->key.dtype == AF_F32;
   if (bm == nullptr || bm->full_kv_num == nullptr || bm->full_kv_idx == nullptr ||
       bm->kv_num_blocks == nullptr || bm->kv_indices == nullptr)
     return fail(AF_ERR_BAD_ARG, "block mask lists are NULL");
   if (bm->block_m != 32 && bm->block_m != 64 && bm->block_m != 128)
     return fail(AF_ERR_UNSUPPORTED, "block-sparse BLOCK_M=%d: supported 32, 64, 128", bm->block_m);
-  if (bm->block_n <= 0 || bm->block_n % kKeysPerStage != 0)
-    return fail(AF_ERR_UNSUPPORTED, "block-sparse BLOCK_N=%d: must be a multiple of 64", bm->block_n);
+  // key blocks are walked in 64-key stages (fp32: 32-key tiles)
+  const int stage = f32 ? 32 : kKeysPerStage;
+  if (bm->block_n <= 0 || bm->block_n % stage != 0)
+    return fail(AF_ERR_UNSUPPORTED, "block-sparse BLOCK_N=%d: must be a multiple of %d", bm->block_n, stage);
   if (bm->n_q_blocks != (a->seqlen_q + bm->block_m - 1) / bm->block_m ||
       bm->n_kv_blocks != (a->seqlen_kv + bm->block_n - 1) / bm->block_n)
     return fail(AF_ERR_BAD_ARG, "block mask grid %dx%d does not match sequence lengths %d/%d", bm->n_q_blocks,
                 bm->n_kv_blocks, a->seqlen_q, a->seqlen_kv);
   if (a->seqlen_q == 0) return AF_OK;
+  if (f32) {
+    if (a->coverage != nullptr)
+      return fail(AF_ERR_UNSUPPORTED, "tile-visit counters are kept by the fp16/bf16 kernels only");
+    return dispatch_fwd_f32(*a, workspace, workspace_bytes, static_cast<hipStream_t>(stream), bm);
+  }
   FwdParams p = make_fwd_params(a, bm->block_m);
+  p.bs_block_m = bm->block_m;
   p.bs_full_num = bm->full_kv_num;
   p.bs_full_idx = bm->full_kv_idx;
   p.bs_part_num = bm->kv_num_blocks;

@@ -244,7 +244,7 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeParams p)
 // output dim t % D and the splits s = t / D (mod 256 / D); the partial sums
 // of the split groups meet in LDS.  All loads of a thread are independent,
 // so the kernel is bound by the (L2-resident) workspace reads, not latency.
-template <class E, int D>
+template <class E, int D, bool F32OUT = false>
 __global__ void __launch_bounds__(256) decode_combine_kernel(const DecodeParams p) {
   constexpr int NG = 256 / D;
   __shared__ float red_acc[NG][D];
@@ -277,7 +277,184 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(const DecodeParams 
       l += red_l[g2];
     }
     const float inv = (l == 0.f) ? 1.f : 1.f / l;
-    p.o[b * p.os[0] + hq * p.os[1] + d] = E::one(a * inv);
+    if constexpr (F32OUT)
+      reinterpret_cast<float*>(p.o)[b * p.os[0] + hq * p.os[1] + d] = a * inv;
+    else
+      p.o[b * p.os[0] + hq * p.os[1] + d] = E::one(a * inv);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 split kernel.  Decode reads every K/V byte once and does 4 FLOP per
+// 4 bytes read, so fp32 FMAs on the VALU keep up with HBM and no fp32 MFMA
+// is needed.  Lane (k, c) = (lane / 8, lane % 8) holds dims [c D/8, (c+1)
+// D/8) of key slot k: a wave covers 8 keys per step, the dot products are
+// finished with three xor shuffles inside each group of 8 lanes, and the
+// running max of a query head is wave-uniform after three more.  A
+// workgroup serves up to kF32DecHeads(D) query heads of one key/value head,
+// so each K/V row is read once for all of them; each wave keeps the K/V rows
+// of its next step in flight while it computes the current one.  The
+// partials (m in log2 units, l, acc) use the 16-bit kernel's workspace
+// layout, so the combine kernel is the same.
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr int f32_decode_heads(int D) { return 64 / (D / 8) < 16 ? 64 / (D / 8) : 16; }
+template <int D>
+constexpr int kF32DecHeads() { return f32_decode_heads(D); }
+
+template <int D, int BIAS>
+__global__ void __launch_bounds__(256) decode_split_f32_kernel(const DecodeParams p) {
+  constexpr int CH = D / 8;                 // dims per lane
+  constexpr int GQ = kF32DecHeads<D>();     // query heads per workgroup
+  __shared__ float red[4][GQ][2 + D];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int kk = lane >> 3, c = lane & 7;
+  const int split = blockIdx.x;
+  int rest = blockIdx.y;
+  const int qc = rest % p.nqc;
+  rest /= p.nqc;
+  const int hk = rest % p.Hkv;
+  const int b = rest / p.Hkv;
+  const int hq0 = hk * p.G + GQ * qc;
+  const int nq = min(GQ, p.G - GQ * qc);    // real query heads in this chunk
+
+  const float* kbase = reinterpret_cast<const float*>(p.k) + b * p.ks[0] + hk * p.ks[1] + CH * c;
+  const float* vbase = reinterpret_cast<const float*>(p.v) + b * p.vs[0] + hk * p.vs[1] + CH * c;
+  // this lane's dims of every query head of the chunk, pre-scaled to log2
+  // units (the scale multiplies the fp32 dot product; no rounding involved)
+  const float c2 = p.scale * kLog2e;
+  float q[GQ][CH];
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) {
+    const float* qr = reinterpret_cast<const float*>(p.q) + b * p.qs[0] + (int64_t)(hq0 + min(g, nq - 1)) * p.qs[1] +
+                      CH * c;
+#pragma unroll
+    for (int e = 0; e < CH; e += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(qr + e);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q[g][e + j] = v[j];
+    }
+  }
+  float slope2[GQ];
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) slope2[g] = BIAS == 1 ? p.slopes[hq0 + min(g, nq - 1)] * kLog2e : 0.f;
+
+  const int s_lo = split * p.split_len;
+  const int s_hi = min(s_lo + p.split_len, p.Nkv);
+  const int nsteps = s_hi > s_lo ? (s_hi - s_lo + 7) / 8 : 0;
+
+  float m[GQ], l[GQ], acc[GQ][CH];
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < CH; ++e) acc[g][e] = 0.f;
+  }
+
+  // rows of key slot kk of step st (clamped to the last key: every load is
+  // in bounds, and scores of keys >= s_hi are masked)
+  auto load = [&](int st, float (&kr)[CH], float (&vr)[CH]) {
+    const int key = min(s_lo + 8 * st + kk, s_hi - 1);
+#pragma unroll
+    for (int e = 0; e < CH; e += 4) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(kbase + (int64_t)key * p.ks[2] + e);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(vbase + (int64_t)key * p.vs[2] + e);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        kr[e + j] = a[j];
+        vr[e + j] = v[j];
+      }
+    }
+  };
+  auto compute = [&](int st, const float (&kr)[CH], const float (&vr)[CH]) {
+    const int key = s_lo + 8 * st + kk;
+    const bool ok = key < s_hi;
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < CH; ++e) d = __builtin_fmaf(q[g][e], kr[e], d);
+      d += __shfl_xor(d, 1, 64);
+      d += __shfl_xor(d, 2, 64);
+      d += __shfl_xor(d, 4, 64);
+      float x = d * c2;
+      if constexpr (BIAS == 1) x -= slope2[g] * (float)abs((p.Nkv - 1) - key);
+      x = ok ? x : -INFINITY;
+      float mx = fmaxf(x, __shfl_xor(x, 8, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m[g], mx);   // wave-uniform
+      if (m_new > m[g]) {
+        const float alpha = __builtin_amdgcn_exp2f(m[g] - m_new);   // 0 while m = -inf
+        l[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < CH; ++e) acc[g][e] *= alpha;
+        m[g] = m_new;
+      }
+      const float pr = (m[g] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x - m[g]);
+      l[g] += pr;
+#pragma unroll
+      for (int e = 0; e < CH; ++e) acc[g][e] = __builtin_fmaf(pr, vr[e], acc[g][e]);
+    }
+  };
+  float ka[CH], va[CH], kb2[CH], vb[CH];
+  if (w < nsteps) load(w, ka, va);
+  for (int st = w; st < nsteps; st += 8) {
+    if (st + 4 < nsteps) load(st + 4, kb2, vb);
+    compute(st, ka, va);
+    if (st + 4 >= nsteps) break;
+    if (st + 8 < nsteps) load(st + 8, ka, va);
+    compute(st + 4, kb2, vb);
+  }
+
+  // ---- per wave: sums over the 8 key slots, then the 4 waves through LDS --
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) {
+    l[g] += __shfl_xor(l[g], 8, 64);
+    l[g] += __shfl_xor(l[g], 16, 64);
+    l[g] += __shfl_xor(l[g], 32, 64);
+#pragma unroll
+    for (int e = 0; e < CH; ++e) {
+      float a = acc[g][e];
+      a += __shfl_xor(a, 8, 64);
+      a += __shfl_xor(a, 16, 64);
+      a += __shfl_xor(a, 32, 64);
+      acc[g][e] = a;
+    }
+  }
+  if (kk == 0) {
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+      if (c == 0) {
+        red[w][g][0] = m[g];
+        red[w][g][1] = l[g];
+      }
+#pragma unroll
+      for (int e = 0; e < CH; ++e) red[w][g][2 + CH * c + e] = acc[g][e];
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < GQ * D; idx += 256) {
+    const int g = idx / D, d = idx - g * D;
+    if (g >= nq) continue;
+    float mstar = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) mstar = fmaxf(mstar, red[ww][g][0]);
+    const float mu = (mstar == -INFINITY) ? 0.f : mstar;
+    float a = 0.f, ls = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float f = __builtin_amdgcn_exp2f(red[ww][g][0] - mu);
+      a += f * red[ww][g][2 + d];
+      ls += f * red[ww][g][1];
+    }
+    const int64_t row = ((int64_t)split * p.B + b) * p.Hq + hq0 + g;
+    p.ws_acc[row * D + d] = a;
+    if (d == 0) {
+      p.ws_ml[2 * row] = mstar;
+      p.ws_ml[2 * row + 1] = ls;
+    }
   }
 }
 

@@ -21,7 +21,8 @@
 // are D/32 consecutive floats.  Every lane owns one query of O^T, so the
 // online-softmax rescale needs no cross-lane traffic.
 //
-// Masks, bias kind, normalisation and RoPE are uniform runtime switches:
+// Masks (block-sparse: the BlockMask row of each wave's 32 queries lists its
+// key blocks), bias kind, normalisation and RoPE are uniform runtime switches:
 // the mask test and bias add are a few VALU instructions per score against
 // 64 cycles per MFMA.  Keys are rotated once per call (rope_f32_kernel) and
 // the query rows once per workgroup, as the 16-bit path does.
@@ -134,6 +135,27 @@ __global__ void __launch_bounds__(kF32Waves * 64) fwd_f32_kernel(const FwdF32Par
     n_hi = min(n_hi, q0 + 32);
   }
   n_lo &= ~31;
+  // 32-key tiles: a range, or with a block mask the tiles of the listed key
+  // blocks of this wave's mask row (32-row waves never straddle two rows)
+  int ntiles = n_hi > n_lo ? (n_hi - n_lo + 31) / 32 : 0;
+  int bs_sub = 1, bs_nfull = 0;
+  const int32_t* bs_full_row = nullptr;
+  const int32_t* bs_part_row = nullptr;
+  if (mask == MASK_BS) {
+    const int mr = q0 / p.bs_block_m;
+    bs_sub = p.bs_block_n / 32;
+    bs_nfull = p.bs_full_num[mr];
+    bs_full_row = p.bs_full_idx + mr * p.bs_full_rs;
+    bs_part_row = p.bs_part_idx + mr * p.bs_part_rs;
+    ntiles = (bs_nfull + p.bs_part_num[mr]) * bs_sub;
+  }
+  auto tile_n0 = [&](int t) -> int {
+    if (mask == MASK_BS) {
+      const int e = t / bs_sub;
+      return bs_row_get(bs_full_row, bs_nfull, bs_part_row, e) * p.bs_block_n + 32 * (t - e * bs_sub);
+    }
+    return n_lo + 32 * t;
+  };
 
   const float* kg = reinterpret_cast<const float*>(p.k) + b * p.ks[0] + hk * p.ks[1];
   const float* vg = reinterpret_cast<const float*>(p.v) + b * p.vs[0] + hk * p.vs[1];
@@ -160,9 +182,10 @@ __global__ void __launch_bounds__(kF32Waves * 64) fwd_f32_kernel(const FwdF32Par
 #pragma unroll
     for (int i = 0; i < DH / 4; ++i) kv[i] = *reinterpret_cast<const f32x4*>(kr + 4 * i);
   };
-  if (n_lo < n_hi) load_k(n_lo);
+  if (ntiles > 0) load_k(tile_n0(0));
 
-  for (int n0 = n_lo; n0 < n_hi; n0 += 32) {
+  for (int t = 0; t < ntiles; ++t) {
+    const int n0 = tile_n0(t);
     VecC vv[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -178,7 +201,7 @@ __global__ void __launch_bounds__(kF32Waves * 64) fwd_f32_kernel(const FwdF32Par
 #pragma unroll
       for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[j][e], qv[e], s, 0, 0, 0);
     }
-    load_k(n0 + 32);  // next tile (clamped, so always in bounds)
+    if (t + 1 < ntiles) load_k(tile_n0(t + 1));  // next tile (rows clamped, so in bounds)
 
     float x[16];
     float mt = -INFINITY;

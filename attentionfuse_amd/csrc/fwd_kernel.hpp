@@ -55,7 +55,7 @@ struct FwdParams {
   int64_t qs[4], ks[4], vs[4], os[4], ls[3], rs[2], bs[4];
   int64_t bs_full_rs, bs_part_rs;
   int32_t B, Hq, Hkv, Nq, Nkv, G;
-  int32_t n_mblocks, bs_block_n;
+  int32_t n_mblocks, bs_block_m, bs_block_n;
   int32_t cov_nq, cov_nk;
   int32_t rope_len;
   float scale;

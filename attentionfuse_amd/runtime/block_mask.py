@@ -130,10 +130,10 @@ def _check_mask(Q, K, bm: BlockMask) -> None:
 
 
 def _bs_key(Q, bias_kind: int, rope: bool):
-    dt = {torch.float16: 0, torch.bfloat16: 1}.get(Q.dtype)
+    dt = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}.get(Q.dtype)
     if dt is None:
-        raise NotImplementedError(f"block-sparse kernels take fp16/bf16, "
-                                  f"got {Q.dtype}")
+        raise NotImplementedError(f"block-sparse kernels take fp16, bf16 or "
+                                  f"fp32, got {Q.dtype}")
     return (dt, Q.shape[-1], 3, int(bias_kind), 0, int(rope))
 
 

@@ -32,8 +32,10 @@ def can_use_flash_decode(graph: Graph, Q: torch.Tensor, K: torch.Tensor) -> bool
         return False
     if graph.has_rope or graph.norm().kind is not NormKind.SOFTMAX:
         return False
+    if Q.dtype == torch.float32:
+        return Q.shape[-1] in (32, 64, 128)
     return Q.shape[-1] in (32, 64, 128, 256) and Q.dtype in (torch.float16,
-                                                         torch.bfloat16)
+                                                              torch.bfloat16)
 
 
 def _pick_num_splits(B: int, H_q: int, N_kv: int, H_kv: int | None = None,
@@ -64,7 +66,7 @@ def run_flash_decode(graph: Graph, Q: torch.Tensor, K: torch.Tensor,
     slopes = _slopes_f32(H_q, Q, alibi_slopes) if bias_kind == 1 else None
     Qk, Kk, Vk = kernel_layout(Q), kernel_layout(K), kernel_layout(V)
     a = N.DecodeArgsC()
-    dt = 0 if Q.dtype == torch.float16 else 1
+    dt = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}[Q.dtype]
     a.key = N.SpecKeyC(dt, D, 0, bias_kind, 0, 0)
     a.q, a.k, a.v, a.o = Qk.data_ptr(), Kk.data_ptr(), Vk.data_ptr(), out.data_ptr()
     a.alibi_slopes = N.ptr(slopes)

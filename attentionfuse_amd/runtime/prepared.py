@@ -92,7 +92,7 @@ def prepare_decode(graph: Graph, Q, K, V, *, out=None, num_splits: int = 0,
     ws = torch.empty(nbytes, dtype=torch.uint8, device=Q.device)
     slopes = _slopes_f32(Hq, Q, alibi_slopes) if bundle.bias_kind == 1 else None
     a = N.DecodeArgsC()
-    a.key = N.SpecKeyC(0 if Q.dtype == torch.float16 else 1, D, 0,
+    a.key = N.SpecKeyC({torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}[Q.dtype], D, 0,
                        bundle.bias_kind, 0, 0)
     a.q, a.k, a.v, a.o = Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr()
     a.alibi_slopes = N.ptr(slopes)

@@ -66,7 +66,7 @@ typedef enum af_norm { AF_NORM_SOFTMAX = 0, AF_NORM_RELU = 1 } af_norm;
 /* Specialisation key: replaces the reference's Triton constexpr record
  * (attnfuse/compiler/codegen.py:391-404; attnfuse/ir/tiled.py:52-81). */
 typedef struct af_spec_key {
-  int32_t dtype;     /* af_dtype; AF_F32: af_fwd and af_bwd, not block-sparse or decode */
+  int32_t dtype;     /* af_dtype; AF_F32: every entry point except the block-sparse backward */
   int32_t head_dim;  /* instantiated: 32, 64, 128, 256 (256: fp16/bf16 only; af_query) */
   int32_t mask;      /* af_mask                   */
   int32_t bias;      /* af_bias                   */
@@ -130,7 +130,8 @@ int af_fwd(const af_fwd_args* args, void* workspace, size_t workspace_bytes,
  * (reference: attnfuse/runtime/block_mask.py:205-271,
  * attnfuse/compiler/codegen_blocksparse.py:34-171).  args->key.mask must be
  * AF_MASK_BLOCK_SPARSE; the tile visited per listed block is whole (no
- * element mask inside it, reference semantics). */
+ * element mask inside it, reference semantics).  BLOCK_M 32, 64 or 128;
+ * BLOCK_N a multiple of 64 (fp16/bf16) or of 32 (fp32). */
 int af_fwd_blocksparse(const af_fwd_args* args, const af_blockmask* bm,
                        void* workspace, size_t workspace_bytes, void* stream);
 
@@ -139,7 +140,9 @@ int af_fwd_blocksparse(const af_fwd_args* args, const af_blockmask* bm,
  * attnfuse_decode_combine_kernel (reference:
  * attnfuse/runtime/flash_decode.py:101-187,
  * attnfuse/compiler/codegen_decode.py:46-211).  key.mask must be FULL and
- * key.bias NONE or ALIBI, key.rope 0. */
+ * key.bias NONE or ALIBI, key.rope 0.  fp16/bf16 run the split on the
+ * 16x16x32 MFMAs; fp32 (head dims 32, 64, 128) on fp32 VALU FMAs, which keep
+ * up with HBM at decode's 1 FLOP per byte. */
 typedef struct af_decode_args {
   af_spec_key key;
   const void* q;  /* (B, H_q, 1, D)     */

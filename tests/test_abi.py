@@ -67,7 +67,7 @@ def test_query_and_tile():
     assert lib.af_query(N.SpecKeyC(0, 64, 1, 1, 0, 1)) == 1
     assert lib.af_query(N.SpecKeyC(1, 128, 3, 0, 0, 0)) == 1
     assert lib.af_query(N.SpecKeyC(2, 64, 1, 1, 1, 1)) == 1      # fp32 forward
-    assert lib.af_query(N.SpecKeyC(2, 64, 3, 0, 0, 0)) == 0      # fp32 block-sparse
+    assert lib.af_query(N.SpecKeyC(2, 64, 3, 0, 0, 0)) == 1      # fp32 block-sparse
     assert lib.af_query(N.SpecKeyC(3, 64, 0, 0, 0, 0)) == 0      # dtype
     assert lib.af_query(N.SpecKeyC(0, 80, 0, 0, 0, 0)) == 0      # head_dim
     bm, bn = C.c_int32(), C.c_int32()
@@ -77,17 +77,27 @@ def test_query_and_tile():
     assert (bm.value, bn.value) == (128, 32)
 
 
-def test_fp32_outside_the_forward_is_rejected():
-    """fp32 has forward and backward kernels but no decode or block-sparse
-    ones: those entry points reject it with an error naming fp16/bf16."""
+def test_fp32_coverage_of_the_entry_points():
+    """fp32 has forward (block-sparse included), decode and backward kernels;
+    the block-sparse backward and head dim 256 refuse it with a message, and
+    decode without a workspace fails on the workspace, not the dtype."""
     lib = N.lib()
+    assert lib.af_query(N.SpecKeyC(2, 64, 3, 0, 0, 0)) == 1      # fp32 block-sparse forward
+    assert lib.af_query(N.SpecKeyC(2, 256, 0, 0, 0, 0)) == 0     # fp32 head dim 256
     a = N.DecodeArgsC()
     a.key = N.SpecKeyC(2, 64, 0, 0, 0, 0)
     a.batch, a.heads_q, a.heads_kv, a.seqlen_kv = 1, 4, 4, 64
     a.q, a.k, a.v, a.o = 256, 256, 256, 256
     for s in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
         s[:] = (64 * 4 * 64, 64 * 64, 64, 1)
+    a.scale = 0.125
+    assert lib.af_decode(a, None, 0, None) == N.AF_ERR_WORKSPACE
+    a.key = N.SpecKeyC(2, 256, 0, 0, 0, 0)
     assert lib.af_decode(a, None, 0, None) == N.AF_ERR_UNSUPPORTED
+    assert "256" in N.last_error()
+    b = N.BwdArgsC()
+    b.key = N.SpecKeyC(2, 64, 3, 0, 0, 0)
+    assert lib.af_bwd(b, None, None, 0, None) == N.AF_ERR_UNSUPPORTED
     assert "fp16 or bf16" in N.last_error()
 
 

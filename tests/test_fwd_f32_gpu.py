@@ -88,3 +88,83 @@ def test_large_scores_stay_finite():
     want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(), causal=True)
     assert torch.isfinite(out).all()
     assert (out.cpu() - want).abs().max().item() <= TOL
+
+
+# ---- fp32 block-sparse forward and fp32 split-K decode ----------------------
+BS_PATTERNS = {
+    "bigbird": lambda q, k: ((q // 64) == 0) | ((k // 64) == 0) | (((q // 64) - (k // 64)).abs() <= 1),
+    "strided": lambda q, k: ((q // 32) + (k // 32)) % 3 == 0,
+    "local": lambda q, k: ((q // 64) - (k // 64)).abs() <= 1,
+}
+
+
+@pytest.mark.parametrize("blocks", [(64, 64), (32, 32), (128, 64), (64, 128), (32, 96)])
+@pytest.mark.parametrize("name", sorted(BS_PATTERNS))
+def test_block_sparse(name, blocks):
+    """fp32 inputs with a BlockMask: the fp32 kernel walks each wave's mask
+    row (block sizes down to 32)."""
+    bm_, bn_ = blocks
+    N = 384
+    Q, K, V = make(2, 4, 4, N, N, 64, F32, seed=11)
+    bm = af.create_block_mask(BS_PATTERNS[name], N, N, bm_, bn_)
+    fn = af.attention(lambda Q, K, V: af.softmax(af.block_sparse(af.scaled_dot_product(Q, K))) @ V)
+    out = fn(Q, K, V, block_mask=bm)
+    torch.cuda.synchronize()
+    grid = O.block_grid(BS_PATTERNS[name], N, N, bm_, bn_)
+    want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(), elem_mask=O.element_mask_from_grid(grid, N, N, bm_, bn_))
+    assert (out.cpu() - want).abs().max().item() <= TOL
+
+
+def test_block_sparse_rope_alibi():
+    N, H = 256, 4
+    Q, K, V = make(1, H, H, N, N, 64, F32, seed=12)
+    cos, sin = build_rope_cache(N, 64, device="cuda", dtype=F32)
+    bm = af.create_block_mask(BS_PATTERNS["bigbird"], N, N, 64, 64)
+    fn = af.attention(lambda Q, K, V: af.softmax(af.block_sparse(af.alibi(af.rope(Q, K), H))) @ V)
+    out = fn(Q, K, V, block_mask=bm, cos=cos, sin=sin)
+    torch.cuda.synchronize()
+    from attnfuse.runtime.dispatch import _alibi_slopes
+    grid = O.block_grid(BS_PATTERNS["bigbird"], N, N, 64, 64)
+    want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(), elem_mask=O.element_mask_from_grid(grid, N, N, 64, 64),
+                             alibi_slopes=_alibi_slopes(H, "cpu", "torch.float32"),
+                             rope=(cos[0, 0].cpu(), sin[0, 0].cpu()))
+    assert (out.cpu() - want).abs().max().item() <= TOL
+
+
+def _decode_inputs(B, Hq, Hkv, N, D, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    Q = torch.randn(B, Hq, 1, D, generator=g, device="cuda", dtype=F32)
+    K = torch.randn(B, Hkv, N, D, generator=g, device="cuda", dtype=F32)
+    V = torch.randn(B, Hkv, N, D, generator=g, device="cuda", dtype=F32)
+    return Q, K, V
+
+
+@pytest.mark.parametrize("shape", [(2, 8, 2, 4096, 128), (1, 32, 8, 3001, 64), (3, 6, 3, 700, 32),
+                                   (1, 32, 2, 2048, 64), (2, 4, 4, 513, 128)])
+def test_decode(shape):
+    """fp32 single-query calls take the split-K decode (VALU split kernel +
+    log-sum-exp combine), GQA groups of 1 to 16 query heads."""
+    B, Hq, Hkv, N, D = shape
+    print(f"[f32 decode] {shape}", flush=True)
+    Q, K, V = _decode_inputs(B, Hq, Hkv, N, D, seed=N)
+    fn = af.attention(lambda Q, K, V: af.softmax(af.scaled_dot_product(Q, K)) @ V)
+    out = fn(Q, K, V)
+    torch.cuda.synchronize()
+    want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu())
+    assert (out.cpu() - want).abs().max().item() <= TOL
+
+
+@pytest.mark.parametrize("splits", [1, 3, 17, 64])
+def test_decode_ragged_splits_and_alibi(splits):
+    from attnfuse.runtime.dispatch import _alibi_slopes
+    from attnfuse.runtime.flash_decode import run_flash_decode
+    B, Hq, Hkv, N, D = 2, 8, 2, 3001, 128
+    Q, K, V = _decode_inputs(B, Hq, Hkv, N, D, seed=splits)
+    fn = af.attention(lambda Q, K, V: af.softmax(af.alibi(af.scaled_dot_product(Q, K), Hq)) @ V)
+    g = fn(Q, K, V, return_graph=True)
+    out = torch.empty_like(Q)
+    run_flash_decode(g, Q, K, V, D ** -0.5, 1, Hkv, out, num_splits=splits)
+    torch.cuda.synchronize()
+    sl = _alibi_slopes(Hq, "cpu", "torch.float32")
+    want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(), alibi_slopes=sl, query_offset=N - 1)
+    assert (out.cpu() - want).abs().max().item() <= TOL
