@@ -371,6 +371,22 @@ __device__ __forceinline__ int tr_at(int lane, int t, int db) {
 // chunks (lane l at chunk l), so each lane fetches the logical chunk that its
 // slot holds under the swizzle.  No data passes through registers.  Rows past
 // the end of a tensor fall outside its resource and load as zeros.
+// off + delta computed next to the load that uses it: as plain C++ the
+// compiler hoists the loop-invariant sums out of the stage loop and holds
+// one register per load again.
+__device__ __forceinline__ uint32_t add_at_use(uint32_t off, uint32_t delta) {
+  uint32_t r;
+  asm volatile("v_add_u32 %0, %1, %2" : "=v"(r) : "s"(delta), "v"(off));
+  return r;
+}
+
+// A wave instruction covers RPI = 512 / D rows.  When a wave's instructions
+// for one tensor lie a multiple of 16 rows apart (the swizzle repeats every
+// 16 rows), their per-lane byte offsets differ by a wave-uniform row delta:
+// the wave then keeps one offset register per tensor and adds the delta per
+// load, instead of one register per instruction.  The delta stays in the
+// vector offset, inside the hardware bounds check that zeroes rows past the
+// end.
 template <int D, int NT, int ROWS = 32>
 struct TileDma {
   static_assert(ROWS % 16 == 0 && ROWS * D % 512 == 0, "whole wave instructions per tile");
@@ -378,17 +394,25 @@ struct TileDma {
   static constexpr int INSTR = 2 * CHUNKS / 64;      // wave instructions per stage
   static constexpr int WAVES = NT / 64;
   static constexpr int IPW = (INSTR + WAVES - 1) / WAVES;
-  uint32_t off[IPW];                                 // byte offsets within rows [r0, r0 + ROWS)
+  static constexpr int RPI = 512 / D;
+  // instructions i < IPW / 2 of every wave load tile A, the rest tile B
+  static constexpr bool SHARED = (INSTR / 2) % WAVES == 0 && (RPI * WAVES) % 16 == 0;
+  uint32_t off[SHARED ? 2 : IPW];                    // byte offsets within rows [r0, r0 + ROWS)
 
+  __device__ static uint32_t lane_off(int m, int lane, int64_t astride, int64_t bstride) {
+    const int pos = 64 * m + lane;
+    const bool isb = pos >= CHUNKS;
+    const int rem = isb ? pos - CHUNKS : pos;
+    const int row = rem / (D / 8), kp = rem % (D / 8);
+    return (uint32_t)((row * (isb ? bstride : astride) + 8 * (kp ^ lds_swz<D>(row))) * 2);
+  }
   __device__ void init(int w, int lane, int64_t astride, int64_t bstride) {
+    if constexpr (SHARED) {
+      off[0] = lane_off(w, lane, astride, bstride);
+      off[1] = lane_off(w + INSTR / 2, lane, astride, bstride);
+    } else {
 #pragma unroll
-    for (int i = 0; i < IPW; ++i) {
-      const int m = w + i * WAVES;
-      const int pos = 64 * m + lane;
-      const bool isb = pos >= CHUNKS;
-      const int rem = isb ? pos - CHUNKS : pos;
-      const int row = rem / (D / 8), kp = rem % (D / 8);
-      off[i] = (uint32_t)((row * (isb ? bstride : astride) + 8 * (kp ^ lds_swz<D>(row))) * 2);
+      for (int i = 0; i < IPW; ++i) off[i] = lane_off(w + i * WAVES, lane, astride, bstride);
     }
   }
   // stage = element offset of the stage inside `lds`
@@ -400,7 +424,14 @@ struct TileDma {
     for (int i = 0; i < IPW; ++i) {
       const int m = w + i * WAVES;   // wave-uniform
       if (INSTR % WAVES != 0 && m >= INSTR) break;
-      buf_ld16_lds(64 * m >= CHUNKS ? br : ar, lds + stage + 512 * m, off[i]);
+      if constexpr (SHARED) {
+        const bool isb = i >= IPW / 2;
+        const int di = isb ? i - IPW / 2 : i;
+        const uint32_t delta = (uint32_t)(di * RPI * WAVES * (isb ? bstride : astride) * 2);
+        buf_ld16_lds(isb ? br : ar, lds + stage + 512 * m, di == 0 ? off[isb ? 1 : 0] : add_at_use(off[isb ? 1 : 0], delta));
+      } else {
+        buf_ld16_lds(64 * m >= CHUNKS ? br : ar, lds + stage + 512 * m, off[i]);
+      }
     }
   }
 };
@@ -413,14 +444,21 @@ struct RowsDma {
   static constexpr int INSTR = CHUNKS / 64;
   static constexpr int WAVES = NT / 64;
   static constexpr int IPW = (INSTR + WAVES - 1) / WAVES;
-  uint32_t off[IPW];
+  static constexpr int RPI = 512 / D;
+  static constexpr bool SHARED = INSTR % WAVES == 0 && (RPI * WAVES) % 16 == 0;
+  uint32_t off[SHARED ? 1 : IPW];
 
+  __device__ static uint32_t lane_off(int m, int lane, int64_t stride) {
+    const int pos = 64 * m + lane;
+    const int row = pos / (D / 8), kp = pos % (D / 8);
+    return (uint32_t)((row * stride + 8 * (kp ^ lds_swz<D>(row))) * 2);
+  }
   __device__ void init(int w, int lane, int64_t stride) {
+    if constexpr (SHARED) {
+      off[0] = lane_off(w, lane, stride);
+    } else {
 #pragma unroll
-    for (int i = 0; i < IPW; ++i) {
-      const int pos = 64 * (w + i * WAVES) + lane;
-      const int row = pos / (D / 8), kp = pos % (D / 8);
-      off[i] = (uint32_t)((row * stride + 8 * (kp ^ lds_swz<D>(row))) * 2);
+      for (int i = 0; i < IPW; ++i) off[i] = lane_off(w + i * WAVES, lane, stride);
     }
   }
   // tile = element offset of the tile inside `lds`
@@ -430,7 +468,11 @@ struct RowsDma {
     for (int i = 0; i < IPW; ++i) {
       const int m = w + i * WAVES;   // wave-uniform
       if (INSTR % WAVES != 0 && m >= INSTR) break;
-      buf_ld16_lds(rs, lds + tile + 512 * m, off[i]);
+      if constexpr (SHARED) {
+        buf_ld16_lds(rs, lds + tile + 512 * m, i == 0 ? off[0] : add_at_use(off[0], (uint32_t)(i * RPI * WAVES * stride * 2)));
+      } else {
+        buf_ld16_lds(rs, lds + tile + 512 * m, off[i]);
+      }
     }
   }
 };
@@ -438,6 +480,25 @@ struct RowsDma {
 // Wait until this wave's loads into LDS have landed (the barrier after it
 // then publishes the whole stage).
 __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Workgroup barrier over LDS tiles that leaves this wave's later loads into
+// LDS in flight.  __syncthreads() is a release/acquire fence pair around
+// s_barrier, and for the release the compiler waits for every outstanding
+// vector memory operation (vmcnt(0)), the loads of stages still ahead
+// included, which serialises any deeper prefetch.  Here the wave's own LDS
+// accesses complete (lgkmcnt(0)) before s_barrier and the "memory" clobber
+// keeps the compiler from moving memory accesses across it; loads into LDS
+// that other waves read after the barrier are waited for (wait_vmcnt)
+// before it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Wait until at most N vector memory operations of this wave are in flight
+// (they complete in issue order): the loads of a later stage may stay
+// outstanding while an earlier stage's have landed.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // ---------------------------------------------------------------------------
 // Entry e (wave-uniform) of one BlockMask row: list a, then list b.  The
@@ -451,5 +512,46 @@ typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
 __device__ inline int bs_row_get(const int32_t* a, int na, const int32_t* b, int e) {
   return e < na ? ((const_i32_ptr)a)[e] : ((const_i32_ptr)b)[e - na];
 }
+
+// The tile starts of one block-sparse walk, held in a register: lane l
+// holds the start of tile l, read by a wave-uniform tile index with
+// v_readlane.  Looked up per stage from the lists instead, every stage's K/V
+// (or Q/dO) loads waited out a scalar load round trip and a division by the
+// tiles per block first.  Tile t of the walk is sub-tile t % sub of entry
+// e0 + t / sub (entries of `blk` rows or keys, sub-tiles of `tile`); tiles
+// from 64 on (walks longer than a work plan's pieces) are looked up in the
+// lists.
+struct BsTiles {
+  int lo;
+  const int32_t* a;
+  const int32_t* b;
+  int na, e0, sub, blk, tile;
+
+  __device__ int lookup(int t) const {
+    const int e = t / sub;
+    return bs_row_get(a, na, b, e0 + e) * blk + (t - e * sub) * tile;
+  }
+  // lanes past the walk's last tile hold 0 and read no list entry
+  __device__ void init(const int32_t* a_, int na_, const int32_t* b_, int e0_, int sub_, int blk_, int tile_,
+                       int ntiles, int lane) {
+    a = a_;
+    na = na_;
+    b = b_;
+    e0 = e0_;
+    sub = sub_;
+    blk = blk_;
+    tile = tile_;
+    auto at = [&](int t) -> int {
+      if (t >= ntiles) return 0;
+      const int e = e0 + t / sub;
+      return (e < na ? a[e] : b[e - na]) * blk + (t % sub) * tile;
+    };
+    lo = at(lane);
+  }
+  __device__ __forceinline__ int operator()(int t) const {
+    if (t < 64) return __builtin_amdgcn_readlane(lo, t);
+    return lookup(t);
+  }
+};
 
 }  // namespace af

@@ -8,6 +8,7 @@
 #include <algorithm>
 
 #include "attnfuse_hip.h"
+#include "bs_split.hpp"
 #include "bwd_f32_kernel.hpp"
 #include "bwd_launch.hpp"
 #include "fwd_f32_kernel.hpp"
@@ -148,6 +149,27 @@ size_t fwd_workspace_bytes(const af_fwd_args& a) {
   const size_t elem = a.key.dtype == AF_F32 ? 4 : 2;
   const size_t bytes = (size_t)a.batch * a.heads_kv * a.seqlen_kv * a.key.head_dim * elem;
   return (bytes + 255) & ~size_t(255);
+}
+
+// Workspace of a block-sparse forward: the rotated keys (RoPE), then with a
+// Q-major work plan the fp32 partials of split rows, (slots, B*Hq, BLOCK_M)
+// rows of D (unnormalised O) and of 2 (running max, row sum).  The fp32
+// kernel walks whole rows and takes no partials.
+struct BsFwdWorkspace {
+  size_t part_o, part_ml, total;
+};
+BsFwdWorkspace bs_fwd_workspace(const af_fwd_args& a, const af_blockmask* bm) {
+  auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
+  BsFwdWorkspace w{0, 0, fwd_workspace_bytes(a)};
+  if (bm == nullptr || bm->q_items == nullptr || bm->n_q_slots <= 0 || a.key.dtype == AF_F32 || a.batch <= 0 ||
+      a.heads_q <= 0 || a.key.head_dim <= 0 || bm->block_m <= 0)
+    return w;
+  const size_t rows = (size_t)bm->n_q_slots * a.batch * a.heads_q * bm->block_m;
+  w.part_o = w.total;
+  w.total += up(rows * a.key.head_dim * sizeof(float));
+  w.part_ml = w.total;
+  w.total += up(rows * 2 * sizeof(float));
+  return w;
 }
 
 // With RoPE, rotate K once into the workspace and point the forward at k~.
@@ -438,7 +460,49 @@ int af_fwd_blocksparse(const af_fwd_args* a, const af_blockmask* bm, void* works
   p.bs_full_rs = bm->full_kv_stride;
   p.bs_part_rs = bm->kv_stride;
   p.bs_block_n = bm->block_n;
-  return dispatch_fwd(p, *a, bm->block_m / 32, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const BsFwdWorkspace wl = bs_fwd_workspace(*a, bm);
+  const bool split = bm->q_items != nullptr && bm->n_q_splits > 0;
+  if (bm->q_items != nullptr) {
+    if ((rc = check_plan(bm->n_q_items, bm->q_splits, bm->n_q_splits, bm->n_q_slots, bm->n_q_blocks, "q")))
+      return rc;
+    if (split && (workspace == nullptr || workspace_bytes < wl.total || !aligned16(workspace)))
+      return fail(AF_ERR_WORKSPACE,
+                  "block-sparse forward with split rows needs a %zu-byte workspace (16-byte aligned; "
+                  "af_fwd_blocksparse_workspace_bytes), got %zu",
+                  wl.total, workspace_bytes);
+    p.bs_items = bm->q_items;
+    p.n_mblocks = bm->n_q_items;  // grid rows: one per plan item
+    if (split) {
+      p.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.part_o);
+      p.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.part_ml);
+    }
+  }
+  if ((rc = dispatch_fwd(p, *a, bm->block_m / 32, workspace, workspace_bytes, s))) return rc;
+  if (!split) return AF_OK;
+  BsFwdCombineParams c;
+  memset(&c, 0, sizeof(c));
+  c.splits = bm->q_splits;
+  c.part_o = p.part_o;
+  c.part_ml = p.part_ml;
+  c.o = static_cast<uint16_t*>(a->o);
+  c.lse = a->lse;
+  for (int i = 0; i < 4; ++i) c.os[i] = a->o_stride[i];
+  for (int i = 0; i < 3; ++i) c.ls[i] = a->lse_stride[i];
+  c.B = a->batch;
+  c.H = a->heads_q;
+  c.Nq = a->seqlen_q;
+  c.BM = bm->block_m;
+  c.softmax = a->key.norm == AF_NORM_SOFTMAX;
+  if (launch_bs_fwd_combine(c, bm->n_q_splits, a->key.dtype, a->key.head_dim, s) != 0)
+    return fail(AF_ERR_UNSUPPORTED, "no block-sparse combine for this key");
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(AF_ERR_LAUNCH, "block-sparse combine launch failed: %s", hipGetErrorString(e));
+  return AF_OK;
+}
+
+size_t af_fwd_blocksparse_workspace_bytes(const af_fwd_args* a, const af_blockmask* bm) {
+  return a == nullptr ? 0 : bs_fwd_workspace(*a, bm).total;
 }
 
 int32_t af_decode_num_splits(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seqlen_kv,
@@ -477,6 +541,11 @@ size_t af_bwd_workspace_bytes(const af_bwd_args* args) {
   return args == nullptr ? 0 : bwd_workspace_bytes(*args);
 }
 
+size_t af_bwd_blocksparse_workspace_bytes(const af_bwd_args* args, const af_blockmask* bm) {
+  if (args == nullptr) return 0;
+  return bwd_workspace_bytes(*args, args->key.mask == AF_MASK_BLOCK_SPARSE ? bm : nullptr);
+}
+
 int af_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_t workspace_bytes,
            void* stream) {
   return run_bwd(a, bm, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
@@ -498,7 +567,8 @@ int af_bwd_tile(const af_bwd_args* a, const af_blockmask* bm, int32_t* block_m, 
   }
   if (block_m) *block_m = bm_rows;
   if (block_n) *block_n = bn_keys;
-  if (group_split) *group_split = a->key.dtype == AF_F32 ? bwd_group_split_f32(*a) : bwd_group_split(*a);
+  if (group_split)
+    *group_split = bwd_group_split_for(*a, a->key.mask == AF_MASK_BLOCK_SPARSE ? bm : nullptr);
   return AF_OK;
 }
 

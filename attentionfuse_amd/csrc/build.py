@@ -42,6 +42,7 @@ UNITS = [
     ("api", "api.hip", []),
     ("decode", "decode_inst.hip", []),
     ("decode_noalloc", "decode_noalloc.hip", []),
+    ("bs_split", "bs_split.hip", []),
     ("bwd", "bwd.hip", []),
     ("fwd_f32", "fwd_f32.hip", []),
     ("bwd_f32", "bwd_f32.hip", []),

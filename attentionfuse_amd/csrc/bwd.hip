@@ -4,6 +4,7 @@
 
 #include <algorithm>
 
+#include "bs_split.hpp"
 #include "bwd_launch.hpp"
 #include "launch.hpp"
 #include "validate.hpp"
@@ -41,9 +42,22 @@ int bwd_group_split_f32(const af_bwd_args& a) {
   return gs;
 }
 
-BwdWorkspace bwd_workspace_layout(const af_bwd_args& a) {
+// The block mask's K-major plan is used when its columns are split and the
+// GQA query heads are not: the library then keeps the heads together (the
+// column pieces already fill the grid) unless the caller asks for a split.
+static bool kv_plan_wanted(const af_bwd_args& a, const af_blockmask* bm) {
+  return bm != nullptr && a.key.mask == AF_MASK_BLOCK_SPARSE && a.key.dtype != AF_F32 && bm->kv_items != nullptr;
+}
+
+int bwd_group_split_for(const af_bwd_args& a, const af_blockmask* bm) {
+  if (a.key.dtype == AF_F32) return bwd_group_split_f32(a);
+  if (kv_plan_wanted(a, bm) && bm->n_kv_splits > 0 && a.group_split == 0) return 1;
+  return bwd_group_split(a);
+}
+
+BwdWorkspace bwd_workspace_layout(const af_bwd_args& a, const af_blockmask* bm) {
   auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
-  BwdWorkspace w{0, 0, 0, 0, 0, 0, 1};
+  BwdWorkspace w{0, 0, 0, 0, 0, 0, 0, 0, 0, 1, false, false};
   if (a.batch <= 0 || a.heads_q <= 0 || a.heads_kv <= 0 || a.seqlen_q < 0 || a.seqlen_kv < 0 || a.key.head_dim <= 0)
     return w;
   const size_t rows_q = (size_t)a.batch * a.heads_q * a.seqlen_q;
@@ -57,18 +71,33 @@ BwdWorkspace bwd_workspace_layout(const af_bwd_args& a) {
     w.kr = w.total;
     w.total += up(rows_k * a.key.head_dim * elem);
   }
-  w.g_split = a.key.dtype == AF_F32 ? bwd_group_split_f32(a) : bwd_group_split(a);
+  w.g_split = bwd_group_split_for(a, bm);
   if (w.g_split > 1) {
     w.dkp = w.total;
     w.total += up((size_t)w.g_split * rows_k * a.key.head_dim * 4);
     w.dvp = w.total;
     w.total += up((size_t)w.g_split * rows_k * a.key.head_dim * 4);
   }
+  // block-sparse work plans: partial rows of the split lists
+  if (bm != nullptr && a.key.mask == AF_MASK_BLOCK_SPARSE && a.key.dtype != AF_F32) {
+    w.q_plan = bm->q_items != nullptr;
+    w.kv_plan = kv_plan_wanted(a, bm) && w.g_split == 1;
+    if (w.q_plan && bm->n_q_slots > 0) {
+      w.pdq = w.total;
+      w.total += up((size_t)bm->n_q_slots * a.batch * a.heads_q * bm->block_m * a.key.head_dim * 4);
+    }
+    if (w.kv_plan && bm->n_kv_slots > 0) {
+      const size_t part = up((size_t)bm->n_kv_slots * a.batch * a.heads_kv * bm->block_n * a.key.head_dim * 4);
+      w.pdk = w.total;
+      w.pdv = w.total + part;
+      w.total += 2 * part;
+    }
+  }
   if (rows_q == 0 && rows_k == 0) w.total = 0;
   return w;
 }
 
-size_t bwd_workspace_bytes(const af_bwd_args& a) { return bwd_workspace_layout(a).total; }
+size_t bwd_workspace_bytes(const af_bwd_args& a, const af_blockmask* bm) { return bwd_workspace_layout(a, bm).total; }
 
 static int bad(int code, const char* msg) {
   set_error("%s", msg);
@@ -128,10 +157,21 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
                !fits(a->seqlen_kv, a->k_stride[2]) || !fits(a->seqlen_kv, a->v_stride[2]) ||
                (k.rope && !fits(a->rope_len, a->rope_stride[0]))))
     return bad(AF_ERR_UNSUPPORTED, "a (batch, head) slice spans 4 GiB or more");
-  const BwdWorkspace wl = bwd_workspace_layout(*a);
+  if (k.mask == AF_MASK_BLOCK_SPARSE && bm != nullptr) {
+    if (bm->q_items != nullptr &&
+        (rc = check_plan(bm->n_q_items, bm->q_splits, bm->n_q_splits, bm->n_q_slots, bm->n_q_blocks, "q")))
+      return rc;
+    if (bm->kv_items != nullptr &&
+        (rc = check_plan(bm->n_kv_items, bm->kv_splits, bm->n_kv_splits, bm->n_kv_slots, bm->n_kv_blocks, "kv")))
+      return rc;
+  }
+  const BwdWorkspace wl = bwd_workspace_layout(*a, k.mask == AF_MASK_BLOCK_SPARSE ? bm : nullptr);
   const size_t need = wl.total;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
-    return bad(AF_ERR_WORKSPACE, "backward workspace too small (af_bwd_workspace_bytes)");
+    return bad(AF_ERR_WORKSPACE,
+               k.mask == AF_MASK_BLOCK_SPARSE
+                   ? "backward workspace too small (af_bwd_blocksparse_workspace_bytes)"
+                   : "backward workspace too small (af_bwd_workspace_bytes)");
 
   BwdParams p;
   memset(&p, 0, sizeof(p));
@@ -226,6 +266,17 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
     p.bs_q_rs = bm->q_stride;
     p.bs_block_m = bm->block_m;
     p.bs_block_n = bm->block_n;
+    if (wl.q_plan) {
+      p.bs_q_items = bm->q_items;
+      if (wl.pdq) p.part_dq = reinterpret_cast<float*>(ws + wl.pdq);
+    }
+    if (wl.kv_plan) {
+      p.bs_kv_items = bm->kv_items;
+      if (wl.pdk) {
+        p.part_dk = reinterpret_cast<float*>(ws + wl.pdk);
+        p.part_dv = reinterpret_cast<float*>(ws + wl.pdv);
+      }
+    }
   }
   if (a->seqlen_q == 0 && a->seqlen_kv == 0) return AF_OK;
   if (f32) {
@@ -244,8 +295,11 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
                        (k.rope ? (int64_t)a->batch * a->heads_kv * a->seqlen_kv : 0);
   const int rpb = 256 / (k.head_dim / 16);
   g.prep = (unsigned)std::max<int64_t>(1, (rows + rpb - 1) / rpb);
-  g.dkv = (unsigned)std::max(1, p.n_kblocks * p.g_split * a->batch * a->heads_kv);
-  g.dq = (unsigned)std::max(1, p.n_qblocks * a->batch * a->heads_q);
+  // grid rows: key (query) blocks, or the block-sparse plans' items
+  const int kv_rows = p.bs_kv_items != nullptr ? bm->n_kv_items : p.n_kblocks;
+  const int q_rows = p.bs_q_items != nullptr ? bm->n_q_items : p.n_qblocks;
+  g.dkv = (unsigned)std::max(1, kv_rows * p.g_split * a->batch * a->heads_kv);
+  g.dq = (unsigned)std::max(1, q_rows * a->batch * a->heads_q);
   g.combine = 0;
   if (p.g_split > 1) {
     const int64_t krows = (int64_t)a->batch * a->heads_kv * a->seqlen_kv;
@@ -273,6 +327,35 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
       break;
   }
   if (r != 0) return bad(AF_ERR_UNSUPPORTED, "no backward instantiation for this key");
+  // sums of the split lists' pieces: one launch for dQ, dV and dK
+  BsGradCombineParams c;
+  memset(&c, 0, sizeof(c));
+  c.B = p.B;
+  c.cos = p.cos;
+  c.sin = p.sin;
+  c.rs = p.rs[0];
+  auto add = [&](const int32_t* splits, int n_splits, const float* part, uint16_t* out, const int64_t* os, int H,
+                 int Nrows, int blk, float scale, bool rope) {
+    BsGradTarget& t = c.t[c.n_targets++];
+    t.splits = splits;
+    t.n_splits = n_splits;
+    t.part = part;
+    t.out = out;
+    for (int i = 0; i < 3; ++i) t.os[i] = os[i];
+    t.H = H;
+    t.N = Nrows;
+    t.BLK = blk;
+    t.scale = scale;
+    t.rope = rope;
+  };
+  if (p.part_dq != nullptr && bm->n_q_splits > 0)
+    add(bm->q_splits, bm->n_q_splits, p.part_dq, p.dq, p.dqs, p.Hq, p.Nq, bm->block_m, p.scale, k.rope != 0);
+  if (p.part_dk != nullptr && bm->n_kv_splits > 0) {
+    add(bm->kv_splits, bm->n_kv_splits, p.part_dv, p.dv, p.dvs, p.Hkv, p.Nkv, bm->block_n, 1.f, false);
+    add(bm->kv_splits, bm->n_kv_splits, p.part_dk, p.dk, p.dks, p.Hkv, p.Nkv, bm->block_n, p.scale, k.rope != 0);
+  }
+  if (c.n_targets > 0) r = launch_bs_grad_combine(c, k.dtype, k.head_dim, stream);
+  if (r != 0) return bad(AF_ERR_UNSUPPORTED, "no block-sparse combine for this key");
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("backward launch failed: %s", hipGetErrorString(e));

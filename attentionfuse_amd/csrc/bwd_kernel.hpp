@@ -88,6 +88,17 @@ struct BwdParams {
   int32_t g_split;
   float* dkp;
   float* dvp;
+  // Block-sparse work plans (nullable): grid row i of the dQ kernel is item
+  // i of bs_q_items, of the dK/dV kernel item i of bs_kv_items (list, first
+  // entry, entries, slot); slot >= 0 writes fp32 partial sums (unscaled,
+  // rotated space) to part_dq (slot, B*Hq, BLOCK_M, D) or part_dk / part_dv
+  // (slot, B*Hkv, BLOCK_N, D) for bs_grad_combine_kernel.  The K-major plan
+  // is used with g_split == 1 only.
+  const int32_t* bs_q_items;
+  const int32_t* bs_kv_items;
+  float* part_dq;
+  float* part_dk;
+  float* part_dv;
   float scale;
 };
 
@@ -294,8 +305,17 @@ __device__ __forceinline__ bool visible(int i, int j, int Nq, int Nkv, int W) {
 // ---------------------------------------------------------------------------
 // dK / dV
 // ---------------------------------------------------------------------------
+// Head dims up to 64: three waves per SIMD (168 VGPRs), which the 4-wave
+// workgroups meet by themselves and the 2-wave block-sparse ones miss by a
+// register.
+template <int D>
+constexpr int bwd_dkv_waves_per_eu() {
+  return D <= 64 ? 3 : 1;
+}
+
 template <class E, int D, int MASK, int BIAS, bool ROPE, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) {
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(bwd_dkv_waves_per_eu<D>())))
+    bwd_dkv_kernel(const BwdParams p) {
   constexpr int NT = WAVES * 64;
   constexpr int BK = 32 * WAVES;
   constexpr int KS = D / 16, DB = D / 32;
@@ -303,7 +323,12 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   constexpr int TILE = 32 * D;             // one 32-row tile (elements)
   constexpr int STAGE = 2 * TILE + 128;    // q~ tile, dO tile, 32 (L log2 e, delta) pairs
   constexpr int VBLK = VLDS ? BK * D : 0;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE + VBLK];
+  // stages in LDS: the loads of stage t + NS - 1 are issued while stage t
+  // computes.  Head dims from 128 on keep two: with the V block a third
+  // would leave room for one 4-wave workgroup per CU (D = 128), or none
+  // (D = 256).
+  constexpr int NS = D >= 128 ? 2 : 3;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[NS * STAGE + VBLK];
 
   // no keys: nothing to write (the launch still has one workgroup)
   if (p.n_kblocks <= 0) return;
@@ -315,8 +340,19 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   // most query tiles, so they are dispatched first.  Then the head-group
   // split, then (batch, key/value head).
   const int BHK = p.B * p.Hkv;
-  const int kb = blockIdx.x / (BHK * p.g_split);
-  const int rem = blockIdx.x - kb * (BHK * p.g_split);
+  const int kbi = blockIdx.x / (BHK * p.g_split);
+  const int rem = blockIdx.x - kbi * (BHK * p.g_split);
+  // block-sparse plan item: a piece [e0, e0 + ne) of column kb's list
+  int kb = kbi, bs_e0 = 0, bs_ne = -1, bs_slot = -1;
+  if constexpr (MASK == MASK_BS) {
+    if (p.bs_kv_items != nullptr) {
+      const int32_t* it = p.bs_kv_items + 4 * kbi;
+      kb = it[0];
+      bs_e0 = it[1];
+      bs_ne = it[2];
+      bs_slot = it[3];
+    }
+  }
   const int split = rem / BHK;
   const int bhk = rem - split * BHK;
   const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
@@ -330,7 +366,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   u32x4 kf[KS], vf[VLDS ? 1 : KS];
   load_operand_rows<D>(kf, p.kt + b * p.kts[0] + hk * p.kts[1], p.kts[2], key, p.Nkv, h);
   const uint16_t* vbase = p.v + b * p.vs[0] + hk * p.vs[1];
-  uint16_t* const vblk = lds + 2 * STAGE;
+  uint16_t* const vblk = lds + NS * STAGE;
   if constexpr (VLDS) {
     const auto vrs = make_rsrc(vbase, span_bytes<D>(p.Nkv, p.vs[2]));
     // key row r is stored at block row kperm(r), so a wave's V operand reads
@@ -362,14 +398,15 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
     bs_sub = p.bs_block_m / 32;
     bs_n = p.bs_q_num[kb];
     bs_row = p.bs_q_idx + kb * p.bs_q_rs;
-    ntq = bs_n * bs_sub;
+    ntq = (bs_ne >= 0 ? bs_ne : bs_n) * bs_sub;
   } else {
     ntq = m_hi > m_lo ? (m_hi - m_lo + 31) / 32 : 0;
   }
+  BsTiles bst;
+  if constexpr (MASK == MASK_BS) bst.init(bs_row, bs_n, bs_row, bs_e0, bs_sub, p.bs_block_m, 32, ntq, lane);
   auto tile_m0 = [&](int t) -> int {
     if constexpr (MASK == MASK_BS) {
-      const int e = t / bs_sub;
-      return bs_row_get(bs_row, bs_n, bs_row, e) * p.bs_block_m + (t - e * bs_sub) * 32;
+      return bst(t);
     } else {
       return m_lo + 32 * t;
     }
@@ -381,9 +418,11 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   // issue the loads of stage t into LDS slot `slot`: the q~ and dO tiles,
   // and (wave 0) the tile's 32 (L log2 e, delta) pairs; rows past N_q load
   // as zeros
-  auto stage_load = [&](int t, int slot) {
-    const int gi = t / ntq, hq = hq0 + gi;
-    const int m0 = tile_m0(t - gi * ntq);
+  // stage t is query tile tl of head hq0 + gi, t = gi * ntq + tl; the loop
+  // steps (gi, tl) along instead of dividing t by ntq twice per stage
+  auto stage_load = [&](int gi, int tl, int slot) {
+    const int hq = hq0 + gi;
+    const int m0 = tile_m0(tl);
     dma.load(lds, slot * STAGE, w, p.qt + b * p.qts[0] + hq * p.qts[1], p.qts[2], p.Nq,
              p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], p.Nq, m0);
     if (w == 0) {
@@ -403,15 +442,43 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
   constexpr bool kAlibiOneSided = BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW);
   const int qr_row = kperm(c);   // tile row of this lane's (permuted) query
 
-  if (ntiles > 0) stage_load(0, 0);
-  wait_lds_dma();
-  __syncthreads();
+  // (head, query tile) of the stage computed (gi, tl) and of the next one to
+  // load (gl, ll)
+  auto adv = [&](int& g, int& l) {
+    if (++l == ntq) {
+      l = 0;
+      ++g;
+    }
+  };
+  int gi = 0, tl = 0, gl = 0, ll = 0;
+  auto load_next = [&](int slot) {
+    stage_load(gl, ll, slot);
+    adv(gl, ll);
+  };
+  // a stage is IPW loads per wave, plus the (L, delta) pairs on wave 0;
+  // waiting for all but the newest stage leaves that many in flight
+  static_assert(decltype(dma)::INSTR % WAVES == 0, "equal loads per wave");
+  constexpr int kStageLoads = decltype(dma)::IPW;
+  auto wait_all_but_newest = [&]() {
+    if (w == 0) wait_vmcnt<kStageLoads + 1>();
+    else wait_vmcnt<kStageLoads>();
+  };
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i)
+    if (i < ntiles) load_next(i);
+  if (NS > 2 && ntiles > 1) wait_all_but_newest();
+  else wait_lds_dma();
+  lds_barrier();
+  int slot = 0;
   for (int t = 0; t < ntiles; ++t) {
-    const bool more = t + 1 < ntiles;
-    if (more) stage_load(t + 1, (t + 1) & 1);
-    const int gi = t / ntq, hq = hq0 + gi;
-    const int m0 = tile_m0(t - gi * ntq);
-    const uint16_t* buf = lds + (t & 1) * STAGE;
+    // stage t + NS - 1 goes to the slot stage t - 1 used; the barrier
+    // closing step t - 1 ended its reads
+    const bool ahead = t + NS - 1 < ntiles;
+    if (ahead) load_next(slot == 0 ? NS - 1 : slot - 1);
+    const int hq = hq0 + gi;
+    const int m0 = tile_m0(tl);
+    adv(gi, tl);
+    const uint16_t* buf = lds + slot * STAGE;
     const uint16_t* Qs = buf;
     const uint16_t* Os = buf + TILE;
     const float* LD = reinterpret_cast<const float*>(buf + 2 * TILE);
@@ -441,24 +508,29 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
       if constexpr (MASK == MASK_SW)
         need_mask = need_mask || m0 + 31 - n0w >= p.window || n0w + 31 - m0 >= p.window;
       if constexpr (MASK == MASK_CSW) need_mask = need_mask || n0w + 31 > m0 || m0 + 31 - n0w >= p.window;
-      // logits in log2 units: register r holds query m0 + 16 (r/8) + 8h + r%8
+      // logits in log2 units (register r holds query m0 + 16 (r/8) + 8h +
+      // r%8); without a bias the raw scores go through the mask (-inf stays
+      // -inf under the positive scale) and the exponent below takes s c2 - L
+      // in one fma
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        // causal-type masks see only j <= i, where -slope |i - j| is linear
-        // in the query index (one add per element)
-        float abias = 0.f;
-        if constexpr (kAlibiOneSided) abias = slope2 * (float)(key - (m0 + 16 * j + 8 * h));
+        if constexpr (BIAS == BIAS_ALIBI) {
+          // causal-type masks see only j <= i, where -slope |i - j| is
+          // linear in the query index (one add per element)
+          float abias = 0.f;
+          if constexpr (kAlibiOneSided) abias = slope2 * (float)(key - (m0 + 16 * j + 8 * h));
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int r = 8 * j + e;
-          float x = s[r] * c2;
-          if constexpr (kAlibiOneSided) {
-            x += abias;
-            abias -= slope2;
-          } else if constexpr (BIAS == BIAS_ALIBI) {
-            x -= slope2 * (float)abs(m0 + 16 * j + 8 * h + e - key);
+          for (int e = 0; e < 8; ++e) {
+            const int r = 8 * j + e;
+            float x = s[r] * c2;
+            if constexpr (kAlibiOneSided) {
+              x += abias;
+              abias -= slope2;
+            } else {
+              x -= slope2 * (float)abs(m0 + 16 * j + 8 * h + e - key);
+            }
+            s[r] = x;
           }
-          s[r] = x;
         }
       }
       if (need_mask) {
@@ -471,7 +543,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
       u32x4 pp[2], pd[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        // pairs of tile rows 16 j + 8 h .. + 7
+        // (L log2 e, delta) pairs of tile rows 16 j + 8 h .. + 7
         f32x4 ld4[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) ld4[i] = *reinterpret_cast<const f32x4*>(LD + 2 * (16 * j + 8 * h) + 4 * i);
@@ -481,7 +553,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
           const int r = 8 * j + e;
           const float L2 = ld4[e >> 1][2 * (e & 1)];
           const float dl = ld4[e >> 1][2 * (e & 1) + 1];
-          const float pr = __builtin_amdgcn_exp2f(s[r] - L2);
+          const float x = BIAS == BIAS_ALIBI ? s[r] - L2 : __builtin_fmaf(s[r], c2, -L2);
+          const float pr = __builtin_amdgcn_exp2f(x);
           pv[e] = pr;
           dsv[e] = pr * (dp[r] - dl);
         }
@@ -507,12 +580,24 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_kernel(const BwdParams p) 
         }
       }
     }
-    wait_lds_dma();
-    __syncthreads();
+    // stage t + 1 has landed in every wave (stage t + 2 may be in flight)
+    if (NS > 2 && ahead) wait_all_but_newest();
+    else wait_lds_dma();
+    lds_barrier();
+    slot = slot + 1 == NS ? 0 : slot + 1;
   }
 
   uint16_t* dkb = p.dk + b * p.dks[0] + hk * p.dks[1];
   uint16_t* dvb = p.dv + b * p.dvs[0] + hk * p.dvs[1];
+  if (MASK == MASK_BS && bs_slot >= 0) {
+    // a piece of a split column
+    if (key < p.Nkv) {
+      const int64_t row = ((int64_t)bs_slot * BHK + bhk) * BK + (key - n0);
+      store_partial_row<D>(dv, p.part_dv + row * D, h);
+      store_partial_row<D>(dk, p.part_dk + row * D, h);
+    }
+    return;
+  }
   if (p.g_split > 1) {
     if (key < p.Nkv) {
       const int64_t row = (((int64_t)split * p.B + b) * p.Hkv + hk) * p.Nkv + key;
@@ -535,7 +620,9 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   constexpr int KS = D / 16, DB = D / 32;
   constexpr int TILE = 32 * D;
   constexpr int STAGE = 2 * TILE;   // k~ tile, v tile
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+  // stages in LDS: the loads of stage t + 2 are issued while stage t computes
+  constexpr int NS = 3;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[NS * STAGE];
 
   // no queries: nothing to write (the launch still has one workgroup)
   if (p.n_qblocks <= 0) return;
@@ -547,7 +634,18 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   const int bh = blockIdx.x % BH;
   const int mbi = blockIdx.x / BH;
   const bool heavy_last = MASK == MASK_CAUSAL || MASK == MASK_CSW;
-  const int mb = heavy_last ? (p.n_qblocks - 1 - mbi) : mbi;
+  // block-sparse plan item: a piece [e0, e0 + ne) of row mb's list
+  int mb = heavy_last ? (p.n_qblocks - 1 - mbi) : mbi;
+  int bs_e0 = 0, bs_ne = -1, bs_slot = -1;
+  if constexpr (MASK == MASK_BS) {
+    if (p.bs_q_items != nullptr) {
+      const int32_t* it = p.bs_q_items + 4 * mbi;
+      mb = it[0];
+      bs_e0 = it[1];
+      bs_ne = it[2];
+      bs_slot = it[3];
+    }
+  }
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.G;
   const int m0 = mb * BMq, q0w = m0 + 32 * w, qrow = q0w + c;
 
@@ -580,14 +678,16 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
     bs_npart = p.bs_part_num[mb];
     bs_full_row = p.bs_full_idx + mb * p.bs_full_rs;
     bs_part_row = p.bs_part_idx + mb * p.bs_part_rs;
-    ntiles = (bs_nfull + bs_npart) * bs_sub;
+    ntiles = (bs_ne >= 0 ? bs_ne : bs_nfull + bs_npart) * bs_sub;
   } else {
     ntiles = n_hi > n_lo ? (n_hi - n_lo + 31) / 32 : 0;
   }
+  BsTiles bst;
+  if constexpr (MASK == MASK_BS)
+    bst.init(bs_full_row, bs_nfull, bs_part_row, bs_e0, bs_sub, p.bs_block_n, 32, ntiles, lane);
   auto tile_n0 = [&](int t) -> int {
     if constexpr (MASK == MASK_BS) {
-      const int e = t / bs_sub;
-      return bs_row_get(bs_full_row, bs_nfull, bs_part_row, e) * p.bs_block_n + (t - e * bs_sub) * 32;
+      return bst(t);
     } else {
       return n_lo + 32 * t;
     }
@@ -610,14 +710,22 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   constexpr bool kAlibiOneSided = BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW);
   const int kr_row = kperm(c);   // tile row of this lane's (permuted) key
 
-  if (ntiles > 0) stage_load(0, 0);
-  wait_lds_dma();
-  __syncthreads();
+  static_assert(decltype(dma)::INSTR % WAVES == 0, "equal loads per wave");
+  constexpr int kStageLoads = decltype(dma)::IPW;
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i)
+    if (i < ntiles) stage_load(i, i);
+  if (ntiles > 1) wait_vmcnt<kStageLoads>();
+  else wait_lds_dma();
+  lds_barrier();
+  int slot = 0;
   for (int t = 0; t < ntiles; ++t) {
-    const bool more = t + 1 < ntiles;
-    if (more) stage_load(t + 1, (t + 1) & 1);
+    // stage t + 2 goes to the slot stage t - 1 used; the barrier closing
+    // step t - 1 ended its reads
+    const bool ahead = t + NS - 1 < ntiles;
+    if (ahead) stage_load(t + NS - 1, slot == 0 ? NS - 1 : slot - 1);
     const int n0 = tile_n0(t);
-    const uint16_t* Ks = lds + (t & 1) * STAGE;
+    const uint16_t* Ks = lds + slot * STAGE;
     const uint16_t* Vs = Ks + TILE;
 
     bool active = q0w < p.Nq && n0 >= 0 && n0 < p.Nkv;
@@ -637,20 +745,23 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
       if constexpr (MASK == MASK_SW)
         need_mask = need_mask || q0w + 31 - n0 >= p.window || n0 + 31 - q0w >= p.window;
       if constexpr (MASK == MASK_CSW) need_mask = need_mask || n0 + 31 > q0w || q0w + 31 - n0 >= p.window;
-      // logits in log2 units: register r holds key n0 + 16 (r/8) + 8h + r%8
+      // logits minus L in log2 units (one fma per element without a bias):
+      // register r holds key n0 + 16 (r/8) + 8h + r%8
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         float abias = 0.f;
-        if constexpr (kAlibiOneSided) abias = slope2 * (float)(n0 + 16 * j + 8 * h - qrow);
+        if constexpr (kAlibiOneSided) abias = slope2 * (float)(n0 + 16 * j + 8 * h - qrow) - L2;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int r = 8 * j + e;
-          float x = s[r] * c2;
+          float x;
           if constexpr (kAlibiOneSided) {
-            x += abias;
+            x = __builtin_fmaf(s[r], c2, abias);
             abias += slope2;
           } else if constexpr (BIAS == BIAS_ALIBI) {
-            x -= slope2 * (float)abs(qrow - (n0 + 16 * j + 8 * h + e));
+            x = __builtin_fmaf(s[r], c2, -L2) - slope2 * (float)abs(qrow - (n0 + 16 * j + 8 * h + e));
+          } else {
+            x = __builtin_fmaf(s[r], c2, -L2);
           }
           s[r] = x;
         }
@@ -669,7 +780,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int r = 8 * j + e;
-          const float pr = __builtin_amdgcn_exp2f(s[r] - L2);
+          const float pr = __builtin_amdgcn_exp2f(s[r]);
           dsv[e] = pr * (dp[r] - dl);
         }
 #pragma unroll
@@ -687,10 +798,18 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
         }
       }
     }
-    wait_lds_dma();
-    __syncthreads();
+    // stage t + 1 has landed in every wave (stage t + 2 may be in flight)
+    if (ahead) wait_vmcnt<kStageLoads>();
+    else wait_lds_dma();
+    lds_barrier();
+    slot = slot + 1 == NS ? 0 : slot + 1;
   }
 
+  if (MASK == MASK_BS && bs_slot >= 0) {
+    // a piece of a split row
+    if (qrow < p.Nq) store_partial_row<D>(dq, p.part_dq + (((int64_t)bs_slot * BH + bh) * BMq + (qrow - m0)) * D, h);
+    return;
+  }
   store_grad_rows<E, D, ROPE>(dq, p.dq + b * p.dqs[0] + hq * p.dqs[1], p.dqs[2], qrow, p.Nq, p.scale, p.cos,
                               p.sin, p.rs[0], h);
 }

@@ -19,9 +19,13 @@ struct BwdGrids {
 // q~ (B*Hq*Nq*D) and k~ (B*Hkv*Nkv*D) in the input dtype, then with a
 // head-group split the fp32 dK and dV partials (g_split*B*Hkv*Nkv*D each);
 // each section 256-byte aligned.
+// With a block mask's work plans, the fp32 partials of split lists follow:
+// dQ rows (Q-major slots, B*Hq, BLOCK_M, D), then dK and dV rows (K-major
+// slots, B*Hkv, BLOCK_N, D) each.
 struct BwdWorkspace {
-  size_t ld, qr, kr, dkp, dvp, total;   // byte offsets and size
+  size_t ld, qr, kr, dkp, dvp, pdq, pdk, pdv, total;   // byte offsets and size
   int g_split;
+  bool q_plan, kv_plan;   // the dQ / dK-dV launches walk the mask's plans
 };
 // Workgroups of the dK/dV kernel per key block and key/value head: the
 // query heads of a group are split (a power of two dividing G) while the
@@ -33,8 +37,11 @@ struct BwdWorkspace {
 int bwd_group_split(const af_bwd_args& a);
 bool group_split_valid(const af_bwd_args& a);
 int bwd_group_split_f32(const af_bwd_args& a);
-BwdWorkspace bwd_workspace_layout(const af_bwd_args& a);
-size_t bwd_workspace_bytes(const af_bwd_args& a);
+// The split the launch uses: fp32's, 1 for a block mask whose K-major plan
+// splits columns (unless the caller sets group_split), else bwd_group_split.
+int bwd_group_split_for(const af_bwd_args& a, const af_blockmask* bm);
+BwdWorkspace bwd_workspace_layout(const af_bwd_args& a, const af_blockmask* bm = nullptr);
+size_t bwd_workspace_bytes(const af_bwd_args& a, const af_blockmask* bm = nullptr);
 int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_t workspace_bytes,
             hipStream_t stream);
 

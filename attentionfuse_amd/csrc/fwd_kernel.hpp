@@ -52,6 +52,13 @@ struct FwdParams {
   const int32_t* bs_full_idx;
   const int32_t* bs_part_num;
   const int32_t* bs_part_idx;
+  // Block-sparse work plan (nullable): item i of (row block, first entry,
+  // entries, slot) is grid row i; slot >= 0 writes the piece's unnormalised
+  // O to part_o and its (running max, row sum) to part_ml, both indexed
+  // (slot, B*Hq, BLOCK_M), for the combine kernel.
+  const int32_t* bs_items;
+  float* part_o;
+  float* part_ml;
   int64_t qs[4], ks[4], vs[4], os[4], ls[3], rs[2], bs[4];
   int64_t bs_full_rs, bs_part_rs;
   int32_t B, Hq, Hkv, Nq, Nkv, G;
@@ -100,7 +107,18 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   const int bh = blockIdx.x % BH;
   const int mbi = blockIdx.x / BH;
   const bool heavy_last = MASK == MASK_CAUSAL || MASK == MASK_CSW;
-  const int mb = heavy_last ? (p.n_mblocks - 1 - mbi) : mbi;
+  // block-sparse plan item: a piece [e0, e0 + ne) of row mb's list
+  int mb = heavy_last ? (p.n_mblocks - 1 - mbi) : mbi;
+  int bs_e0 = 0, bs_ne = -1, bs_slot = -1;
+  if constexpr (MASK == MASK_BS) {
+    if (p.bs_items != nullptr) {
+      const int32_t* it = p.bs_items + 4 * mbi;
+      mb = it[0];
+      bs_e0 = it[1];
+      bs_ne = it[2];
+      bs_slot = it[3];
+    }
+  }
   const int b = bh / p.Hq;
   const int hq = bh - b * p.Hq;
   const int hk = hq / p.G;
@@ -159,14 +177,16 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     bs_npart = p.bs_part_num[mb];
     bs_full_row = p.bs_full_idx + mb * p.bs_full_rs;
     bs_part_row = p.bs_part_idx + mb * p.bs_part_rs;
-    ntiles = (bs_nfull + bs_npart) * bs_sub;
+    ntiles = (bs_ne >= 0 ? bs_ne : bs_nfull + bs_npart) * bs_sub;
   } else {
     ntiles = n_hi > n_lo ? (n_hi - n_lo + BN - 1) / BN : 0;
   }
+  BsTiles bst;
+  if constexpr (MASK == MASK_BS)
+    bst.init(bs_full_row, bs_nfull, bs_part_row, bs_e0, bs_sub, p.bs_block_n, BN, ntiles, lane);
   auto tile_n0 = [&](int t) -> int {
     if constexpr (MASK == MASK_BS) {
-      const int e = t / bs_sub, s = t - e * bs_sub;
-      return bs_row_get(bs_full_row, bs_nfull, bs_part_row, e) * p.bs_block_n + s * BN;
+      return bst(t);
     } else {
       return n_lo + t * BN;
     }
@@ -653,6 +673,21 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // this lane's 32 keys of every tile, plus the partner lane's 32
   float lt = lsum[0] + lsum[1];
   lt += xor32(lt);
+  if (MASK == MASK_BS && bs_slot >= 0) {
+    // a piece of a split row: unnormalised O and (m, l) for the combine
+    if (qrow < p.Nq) {
+      const int64_t prow = ((int64_t)bs_slot * BH + bh) * BM + (qrow - m0);
+      float* orow = p.part_o + prow * D;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4*>(orow + 32 * db + 8 * g + 4 * h) =
+              f32x4{o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
+      if (h == 0) *reinterpret_cast<f32x2*>(p.part_ml + 2 * prow) = f32x2{m_run, lt};
+    }
+    return;
+  }
   const float inv = (lt == 0.f) ? 1.f : 1.f / lt;
   if (qrow < p.Nq) {
     uint16_t* orow = p.o + b * p.os[0] + hq * p.os[1] + (int64_t)qrow * p.os[2];

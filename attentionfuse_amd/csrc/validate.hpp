@@ -11,6 +11,18 @@ void set_error(const char* fmt, ...);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// A block-mask work plan as af_blockmask_plan writes it: at least one item
+// per list, and every split (two or more slots) listed.
+inline int check_plan(int n_items, const int32_t* splits, int n_splits, int n_slots, int n_lists,
+                      const char* which) {
+  if (n_items < n_lists || n_splits < 0 || n_slots < 2 * n_splits || (n_splits > 0 && splits == nullptr)) {
+    set_error("block mask %s work plan is inconsistent (%d items for %d lists, %d splits, %d slots)", which,
+              n_items, n_lists, n_splits, n_slots);
+    return AF_ERR_BAD_ARG;
+  }
+  return AF_OK;
+}
+
 // (B, H, N, D) tensor with unit D-stride and 16-byte aligned rows.  A
 // tensor with no rows (N == 0) is never read or written and may be NULL.
 inline int check_bhnd(const char* name, const void* ptr, const int64_t* st, int64_t rows) {

@@ -41,7 +41,13 @@ class BlockMaskC(C.Structure):
                 ("full_kv_stride", C.c_int64), ("kv_stride", C.c_int64),
                 ("q_stride", C.c_int64),
                 ("block_m", C.c_int32), ("block_n", C.c_int32),
-                ("n_q_blocks", C.c_int32), ("n_kv_blocks", C.c_int32)]
+                ("n_q_blocks", C.c_int32), ("n_kv_blocks", C.c_int32),
+                ("q_items", C.c_void_p), ("q_splits", C.c_void_p),
+                ("kv_items", C.c_void_p), ("kv_splits", C.c_void_p),
+                ("n_q_items", C.c_int32), ("n_q_splits", C.c_int32),
+                ("n_q_slots", C.c_int32),
+                ("n_kv_items", C.c_int32), ("n_kv_splits", C.c_int32),
+                ("n_kv_slots", C.c_int32)]
 
 
 class FwdArgsC(C.Structure):
@@ -99,12 +105,18 @@ SIGNATURES = {
     "af_fwd_blocksparse": (C.c_int, [C.POINTER(FwdArgsC),
                                      C.POINTER(BlockMaskC), C.c_void_p,
                                      C.c_size_t, C.c_void_p]),
+    "af_fwd_blocksparse_workspace_bytes": (C.c_size_t, [
+        C.POINTER(FwdArgsC), C.POINTER(BlockMaskC)]),
+    "af_blockmask_plan": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32,
+                                    C.c_void_p, C.c_void_p, C.c_void_p]),
     "af_decode_num_splits": (C.c_int32, [C.c_int32] * 5),
     "af_decode_workspace_bytes": (C.c_size_t, [C.c_int32] * 4),
     "af_decode": (C.c_int, [C.POINTER(DecodeArgsC), C.c_void_p, C.c_size_t,
                             C.c_void_p]),
     "af_decode_noalloc": (C.c_int, [C.POINTER(DecodeArgsC), C.c_void_p]),
     "af_bwd_workspace_bytes": (C.c_size_t, [C.POINTER(BwdArgsC)]),
+    "af_bwd_blocksparse_workspace_bytes": (C.c_size_t, [
+        C.POINTER(BwdArgsC), C.POINTER(BlockMaskC)]),
     "af_bwd": (C.c_int, [C.POINTER(BwdArgsC), C.POINTER(BlockMaskC),
                          C.c_void_p, C.c_size_t, C.c_void_p]),
     "af_bwd_tile": (C.c_int, [C.POINTER(BwdArgsC), C.POINTER(BlockMaskC),
@@ -117,7 +129,7 @@ SIGNATURES = {
     "af_abi_version": (C.c_int, []),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib = None
 _lock = threading.Lock()

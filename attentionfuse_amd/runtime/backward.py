@@ -105,9 +105,10 @@ def _run_backward_key(key, Q, K, V, O, L, dO, sm_scale, window, cos, sin,
     a.scale = float(sm_scale)
     a.window = int(window or 0)
     a.group_split = _group_split_request()
-    nbytes = int(N.lib().af_bwd_workspace_bytes(a))
-    ws = _bwd_workspace(Q.device, nbytes)
     bm = block_mask._c() if block_mask is not None else None
+    nbytes = int(N.lib().af_bwd_workspace_bytes(a) if bm is None else
+                 N.lib().af_bwd_blocksparse_workspace_bytes(a, bm))
+    ws = _bwd_workspace(Q.device, nbytes)
     N.check(N.lib().af_bwd(a, bm, ws.data_ptr(), ws.numel(),
                            N.stream_handle(Q.device)))
     return dQ, dK, dV

@@ -11,15 +11,66 @@ active element is rounded up to fully active), a K-major transpose
 ``create_block_mask`` evaluates the predicate on the (Q_LEN, KV_LEN) index
 grid exactly like the reference, but reduces it to the block grid with one
 reshape + ``any`` instead of a Python loop over tiles.
+
+Beyond the reference fields a mask carries a work plan (``BlockMaskPlan``,
+from ``af_blockmask_plan``): lists much longer than the mean -- BigBird's
+global query block visits every key block, and every query block visits the
+global key block -- are cut into pieces that run as workgroups of their own
+and whose fp32 partials a combine kernel merges, so that one long list no
+longer holds up the end of the grid.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+import ctypes as C
+from dataclasses import dataclass, field
 from typing import Callable, Optional
 
 import torch
 
 from . import _native as N
+
+
+@dataclass
+class BlockMaskPlan:
+    """Work plans of the Q-major lists (forward, dQ) and the K-major lists
+    (dK/dV): items (list, first entry, entries, slot) and splits (list,
+    first slot, slots), int32 on the mask's device."""
+    q_items: torch.Tensor
+    q_splits: torch.Tensor
+    n_q_slots: int
+    kv_items: torch.Tensor
+    kv_splits: torch.Tensor
+    n_kv_slots: int
+
+    def to(self, device) -> "BlockMaskPlan":
+        return BlockMaskPlan(self.q_items.to(device), self.q_splits.to(device),
+                             self.n_q_slots, self.kv_items.to(device),
+                             self.kv_splits.to(device), self.n_kv_slots)
+
+
+def _plan_lists(counts: torch.Tensor, chunk: int = 0):
+    """af_blockmask_plan over host int32 counts -> (items, splits, slots)."""
+    counts = counts.to(torch.int32).cpu().contiguous()
+    n = counts.numel()
+    lib = N.lib()
+    sizes = (C.c_int32 * 3)()
+    cp = C.c_void_p(counts.data_ptr() if n else None)
+    N.check(lib.af_blockmask_plan(cp, n, chunk, None, None, sizes))
+    items = torch.empty(max(sizes[0], 1), 4, dtype=torch.int32)
+    splits = torch.zeros(max(sizes[1], 1), 3, dtype=torch.int32)
+    N.check(lib.af_blockmask_plan(cp, n, chunk, C.c_void_p(items.data_ptr()),
+                                  C.c_void_p(splits.data_ptr()), sizes))
+    return items[: sizes[0]], splits[: sizes[1]], int(sizes[2])
+
+
+def make_plan(q_counts: torch.Tensor, kv_counts: torch.Tensor, device,
+              chunk: int = 0) -> BlockMaskPlan:
+    """Plans for lists of ``q_counts`` (Q-major) and ``kv_counts`` (K-major)
+    entries; ``chunk`` <= 0 lets the library choose the piece length."""
+    qi, qs, qn = _plan_lists(q_counts, chunk)
+    ki, ks, kn = _plan_lists(kv_counts, chunk)
+    return BlockMaskPlan(qi.to(device), qs.to(device), qn, ki.to(device),
+                         ks.to(device), kn)
 
 
 @dataclass
@@ -36,11 +87,26 @@ class BlockMask:
     n_kv_blocks: int
     n_active: int
     n_full: int
+    # work plan of the split walks; made from the list lengths on first use
+    # when the mask was not built by block_mask_from_blocks
+    plan: Optional[BlockMaskPlan] = field(default=None, repr=False,
+                                          compare=False)
 
     def to(self, device) -> "BlockMask":
-        f = {k: (v.to(device) if isinstance(v, torch.Tensor) else v)
+        f = {k: (v.to(device) if isinstance(v, (torch.Tensor, BlockMaskPlan))
+                 else v)
              for k, v in self.__dict__.items()}
         return BlockMask(**f)
+
+    def plan_work(self, chunk: int = 0) -> BlockMaskPlan:
+        """(Re)make the work plan from the list lengths (a host copy of the
+        counts: one synchronisation) with piece length ``chunk`` (<= 0: the
+        library's choice)."""
+        qc = (self.full_kv_num.cpu().to(torch.int64)
+              + self.kv_num_blocks.cpu().to(torch.int64))
+        self.plan = make_plan(qc, self.q_num_blocks.cpu(),
+                              self.full_kv_num.device, chunk)
+        return self.plan
 
     def dense_blocks(self) -> torch.Tensor:
         """(n_q_blocks, n_kv_blocks) bool grid of visited tiles."""
@@ -65,6 +131,15 @@ class BlockMask:
         bm.q_stride = self.q_indices.stride(0)
         bm.block_m, bm.block_n = self.BLOCK_M, self.BLOCK_N
         bm.n_q_blocks, bm.n_kv_blocks = self.n_q_blocks, self.n_kv_blocks
+        pl = self.plan if self.plan is not None else self.plan_work()
+        bm.q_items, bm.q_splits = pl.q_items.data_ptr(), pl.q_splits.data_ptr()
+        bm.kv_items = pl.kv_items.data_ptr()
+        bm.kv_splits = pl.kv_splits.data_ptr()
+        bm.n_q_items, bm.n_q_splits = pl.q_items.shape[0], pl.q_splits.shape[0]
+        bm.n_q_slots = pl.n_q_slots
+        bm.n_kv_items = pl.kv_items.shape[0]
+        bm.n_kv_splits = pl.kv_splits.shape[0]
+        bm.n_kv_slots = pl.n_kv_slots
         return bm
 
 
@@ -90,12 +165,16 @@ def block_mask_from_blocks(active: torch.Tensor, BLOCK_M: int, BLOCK_N: int,
     empty_num = torch.zeros(nqb, dtype=torch.int32)
     empty_idx = torch.zeros(nqb, 1, dtype=torch.int32)
     n = int(full_num.sum())
+    # the plan is made here from the host-side counts, so that launching
+    # the mask never copies them back (and can run under graph capture)
+    plan = (make_plan(full_num, q_num, device)
+            if torch.device(device).type == "cuda" else None)
     return BlockMask(
         kv_num_blocks=empty_num.to(device), kv_indices=empty_idx.to(device),
         full_kv_num=full_num.to(device), full_kv_idx=full_idx.to(device),
         q_num_blocks=q_num.to(device), q_indices=q_idx.to(device),
         BLOCK_M=BLOCK_M, BLOCK_N=BLOCK_N, n_q_blocks=nqb, n_kv_blocks=nkb,
-        n_active=n, n_full=n)
+        n_active=n, n_full=n, plan=plan)
 
 
 def create_block_mask(mask_fn: Callable, Q_LEN: int, KV_LEN: int,
@@ -147,8 +226,7 @@ def run_block_sparse(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
     attnfuse/runtime/block_mask.py:205-210).  ``bias_kind`` 1 = ALiBi.
     ``cos``/``sin`` apply fused RoPE."""
     from .dispatch import (_nbytes, _rows_ok, _slopes_f32, check_qkv,
-                           fill_fwd_args, fwd_workspace, kernel_layout,
-                           rope_tables)
+                           fill_fwd_args, kernel_layout, rope_tables)
     check_qkv(Q, K, V)
     _check_mask(Q, K, block_mask)
     B, H, Nq, D = Q.shape
@@ -166,7 +244,8 @@ def run_block_sparse(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
     fill_fwd_args(a, key, Qk, Kk, Vk, o, save_lse, c, s, slopes, None,
                   coverage, sm_scale, 0)
     bm = block_mask._c()
-    ws = fwd_workspace(a, Q.device)
+    nb = int(N.lib().af_fwd_blocksparse_workspace_bytes(a, bm))
+    ws = torch.empty(nb, dtype=torch.uint8, device=Q.device) if nb else None
     N.check(N.lib().af_fwd_blocksparse(a, bm, N.ptr(ws), _nbytes(ws),
                                        N.stream_handle(Q.device)))
     if o is not out:

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define AF_ABI_VERSION 4
+#define AF_ABI_VERSION 5
 
 typedef enum af_status {
   AF_OK = 0,
@@ -87,7 +87,33 @@ typedef struct af_blockmask {
   const int32_t* q_indices;     /* (n_kv_blocks, q_stride)      */
   int64_t full_kv_stride, kv_stride, q_stride;
   int32_t block_m, block_n, n_q_blocks, n_kv_blocks;
+  /* Optional work plans written by af_blockmask_plan, device int32 (all
+   * NULL / 0: one workgroup per query block and per key block, the
+   * reference's grid).  q_*: the Q-major lists (forward, dQ); kv_*: the
+   * K-major lists (dK/dV).  An item is (list, first entry, entries, partial
+   * slot or -1); a split is (list, first slot, slots). */
+  const int32_t* q_items;   /* (n_q_items, 4)   */
+  const int32_t* q_splits;  /* (n_q_splits, 3)  */
+  const int32_t* kv_items;  /* (n_kv_items, 4)  */
+  const int32_t* kv_splits; /* (n_kv_splits, 3) */
+  int32_t n_q_items, n_q_splits, n_q_slots;
+  int32_t n_kv_items, n_kv_splits, n_kv_slots;
 } af_blockmask;
+
+/* Work plan of a block-sparse walk over lists of counts[i] entries (Q-major:
+ * full_kv_num[i] + kv_num_blocks[i]; K-major: q_num_blocks[i]); host
+ * arrays.  No counterpart in the reference, whose grids run one program per
+ * query block and per key block: there a BigBird global row or column, n
+ * blocks long, is a single program's serial walk behind which the rest of
+ * the grid waits.  Lists longer than `chunk` entries (chunk <= 0: the
+ * library's choice, twice the mean list length and at least 8) are cut into
+ * near-equal pieces, each its own workgroup writing fp32 partial results to
+ * a slot of the workspace that a combine kernel merges.  sizes[0..2] =
+ * (n_items, n_splits, n_slots); items (n_items x 4, longest first) and
+ * splits (n_splits x 3) are written when non-NULL: call once with both NULL
+ * for the sizes. */
+int af_blockmask_plan(const int32_t* counts, int32_t n, int32_t chunk,
+                      int32_t* items, int32_t* splits, int32_t* sizes);
 
 /* Forward attention.  Replaces the attnfuse_fwd_kernel launch
  * (reference: attnfuse/runtime/dispatch.py:69-215, kernel
@@ -134,6 +160,11 @@ int af_fwd(const af_fwd_args* args, void* workspace, size_t workspace_bytes,
  * BLOCK_N a multiple of 64 (fp16/bf16) or of 32 (fp32). */
 int af_fwd_blocksparse(const af_fwd_args* args, const af_blockmask* bm,
                        void* workspace, size_t workspace_bytes, void* stream);
+/* Workspace bytes af_fwd_blocksparse needs: af_fwd_workspace_bytes plus,
+ * with a Q-major work plan (fp16/bf16), per partial slot and (batch, head)
+ * BLOCK_M rows of fp32 (unnormalised O, running max, row sum). */
+size_t af_fwd_blocksparse_workspace_bytes(const af_fwd_args* args,
+                                          const af_blockmask* bm);
 
 /* Flash-decoding (one query row per head, split-K over the cache, then a
  * log-sum-exp combine).  Replaces attnfuse_decode_split_kernel +
@@ -217,6 +248,13 @@ size_t af_bwd_workspace_bytes(const af_bwd_args* args);
  * and windowed masks only, bm must then be NULL). */
 int af_bwd(const af_bwd_args* args, const af_blockmask* bm /* nullable */,
            void* workspace, size_t workspace_bytes, void* stream);
+/* Workspace bytes af_bwd needs with this block mask (nullable): the above
+ * plus the fp32 partials of the mask's work plans, BLOCK_M dQ rows per
+ * Q-major slot and (batch, query head), BLOCK_N dK and dV rows per K-major
+ * slot and (batch, key/value head).  The K-major plan is used only when the
+ * GQA query heads are not split (group_split 1). */
+size_t af_bwd_blocksparse_workspace_bytes(const af_bwd_args* args,
+                                          const af_blockmask* bm);
 
 /* Backward launch shape for these arguments: query rows per dQ workgroup,
  * keys per dK/dV workgroup and the GQA group split the launch uses (the
