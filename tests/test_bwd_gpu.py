@@ -192,6 +192,17 @@ def test_backward_group_split_override(split):
         bwd._BWD_TILE.update(saved)
 
 
+@pytest.mark.parametrize("shape", [(2, 4, 1, 384, 64), (1, 8, 2, 640, 128), (1, 4, 4, 200, 64),
+                                   (2, 6, 2, 1000, 128)])
+def test_causal_block_counts(shape):
+    """Causal backward at odd key-block counts, ragged lengths and GQA groups
+    under the library's head-group split."""
+    B, Hq, Hkv, N, D = shape
+    print(f"[bwd] causal blocks {shape}", flush=True)
+    check(run("rope_causal", B, Hq, Hkv, N, D, torch.bfloat16), torch.bfloat16)
+    check(run("causal", B, Hq, Hkv, N, D, torch.float16), torch.float16)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
 @pytest.mark.parametrize("name", ["causal", "rope_causal", "rope_causal_alibi", "dense", "alibi", "sw"])
 def test_backward_head_dim_256(name, dtype):
