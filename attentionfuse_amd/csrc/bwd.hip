@@ -111,8 +111,6 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   const bool f32 = k.dtype == AF_F32;
   if (k.dtype != AF_F16 && k.dtype != AF_BF16 && !f32)
     return bad(AF_ERR_UNSUPPORTED, "backward takes fp16, bf16 or fp32");
-  if (f32 && k.mask == AF_MASK_BLOCK_SPARSE)
-    return bad(AF_ERR_UNSUPPORTED, "the block-sparse backward takes fp16 or bf16");
   if (!head_dim_supported(k.head_dim)) return bad(AF_ERR_UNSUPPORTED, "backward head_dim must be 32, 64, 128 or 256");
   if (f32 && k.head_dim == 256) return bad(AF_ERR_UNSUPPORTED, "the fp32 backward takes head dims 32, 64 and 128");
   if (k.mask < 0 || k.mask > 4) return bad(AF_ERR_UNSUPPORTED, "unknown mask kind");

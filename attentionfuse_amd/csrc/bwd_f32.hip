@@ -6,14 +6,19 @@
 
 namespace af {
 
+// wkv / wq: waves of the dK/dV and dQ workgroups (4; with a block mask the
+// mask's block sizes / 32, 2 or 4)
 template <int D>
-static void launch_bwd_f32_d(BwdParams p, int mask, int bias, int rope, hipStream_t s) {
+static void launch_bwd_f32_d(BwdParams p, int mask, int bias, int rope, int wkv, int wq, hipStream_t s) {
   const int64_t rows_q = (int64_t)p.B * p.Hq * p.Nq;
   if (rows_q > 0)
     hipLaunchKernelGGL((bwd_prep_f32_kernel<D>), dim3((unsigned)((rows_q + 255) / 256)), dim3(256), 0, s, p);
   const unsigned grid_kv = (unsigned)(p.n_kblocks * p.g_split * p.B * p.Hkv);
   if (grid_kv > 0) {
-    hipLaunchKernelGGL((bwd_dkv_f32_kernel<D>), dim3(grid_kv), dim3(kBwdF32Waves * 64), 0, s, p, mask, bias, rope);
+    if (wkv == 2)
+      hipLaunchKernelGGL((bwd_dkv_f32_kernel<D, 2>), dim3(grid_kv), dim3(128), 0, s, p, mask, bias, rope);
+    else
+      hipLaunchKernelGGL((bwd_dkv_f32_kernel<D, 4>), dim3(grid_kv), dim3(256), 0, s, p, mask, bias, rope);
     if (p.g_split > 1) {
       const int64_t threads = (int64_t)p.B * p.Hkv * p.Nkv * (D / 4);
       hipLaunchKernelGGL((bwd_dkv_combine_f32_kernel<D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
@@ -21,14 +26,21 @@ static void launch_bwd_f32_d(BwdParams p, int mask, int bias, int rope, hipStrea
     }
   }
   const unsigned grid_q = (unsigned)(p.n_qblocks * p.B * p.Hq);
-  if (grid_q > 0)
-    hipLaunchKernelGGL((bwd_dq_f32_kernel<D>), dim3(grid_q), dim3(kBwdF32Waves * 64), 0, s, p, mask, bias, rope);
+  if (grid_q > 0) {
+    if (wq == 2)
+      hipLaunchKernelGGL((bwd_dq_f32_kernel<D, 2>), dim3(grid_q), dim3(128), 0, s, p, mask, bias, rope);
+    else
+      hipLaunchKernelGGL((bwd_dq_f32_kernel<D, 4>), dim3(grid_q), dim3(256), 0, s, p, mask, bias, rope);
+  }
 }
 
 int launch_bwd_f32(BwdParams p, const af_bwd_args& a, hipStream_t s) {
   const int D = a.key.head_dim;
-  p.n_kblocks = (a.seqlen_kv + kBwdF32Block - 1) / kBwdF32Block;
-  p.n_qblocks = (a.seqlen_q + kBwdF32Block - 1) / kBwdF32Block;
+  const bool bs = a.key.mask == AF_MASK_BLOCK_SPARSE;
+  // block-sparse: one workgroup per mask block (p.bs_block_m / _n set by the caller)
+  const int bk = bs ? p.bs_block_n : kBwdF32Block, bq = bs ? p.bs_block_m : kBwdF32Block;
+  p.n_kblocks = (a.seqlen_kv + bk - 1) / bk;
+  p.n_qblocks = (a.seqlen_q + bq - 1) / bq;
   if (a.key.rope) {
     // q~ and k~ (fp32, contiguous) into the workspace copies p.qr / p.kr
     launch_rope_f32(static_cast<const float*>(a.q), reinterpret_cast<float*>(p.qr), static_cast<const float*>(a.cos),
@@ -38,10 +50,11 @@ int launch_bwd_f32(BwdParams p, const af_bwd_args& a, hipStream_t s) {
                     static_cast<const float*>(a.sin), a.k_stride, a.rope_stride[0], a.heads_kv, a.seqlen_kv,
                     (int64_t)a.batch * a.heads_kv * a.seqlen_kv, D, s);
   }
+  const int wkv = bk / 32, wq = bq / 32;
   switch (D) {
-    case 32: launch_bwd_f32_d<32>(p, a.key.mask, a.key.bias, a.key.rope, s); return 0;
-    case 64: launch_bwd_f32_d<64>(p, a.key.mask, a.key.bias, a.key.rope, s); return 0;
-    case 128: launch_bwd_f32_d<128>(p, a.key.mask, a.key.bias, a.key.rope, s); return 0;
+    case 32: launch_bwd_f32_d<32>(p, a.key.mask, a.key.bias, a.key.rope, wkv, wq, s); return 0;
+    case 64: launch_bwd_f32_d<64>(p, a.key.mask, a.key.bias, a.key.rope, wkv, wq, s); return 0;
+    case 128: launch_bwd_f32_d<128>(p, a.key.mask, a.key.bias, a.key.rope, wkv, wq, s); return 0;
   }
   return -1;
 }

@@ -22,6 +22,11 @@
 //                        for the workgroup's four waves: S^T and dP^T with
 //                        keys as the MFMA rows, dS^T, dQ^T += k~^T dS^T.
 //
+// With a block mask (reference: attnfuse/compiler/codegen_blocksparse_bwd.py:
+// 29-233) a workgroup is one mask block (WAVES = block size / 32, 2 or 4):
+// dK/dV walk the K-major list of their key block, dQ the Q-major lists of
+// their query block, in 32-row tiles of the listed blocks, each visited whole.
+//
 // Output block c, row m of dV, dK and dQ^T holds d = (D/32) m + c, so a
 // lane's operand reads and stores are D/32 consecutive floats.  With RoPE
 // the rotated-space gradients are rotated back before the store:
@@ -77,10 +82,10 @@ __device__ __forceinline__ void f32_rope_back(float& lo, float& hi, float clo, f
   hi = b;
 }
 
-template <int D>
-__global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const BwdParams p, int mask, int bias,
-                                                                         int rope) {
+template <int D, int WAVES = kBwdF32Waves>
+__global__ void __launch_bounds__(WAVES * 64) bwd_dkv_f32_kernel(const BwdParams p, int mask, int bias, int rope) {
   constexpr int DH = D / 2, DC = D / 32, QP = D + 4;
+  constexpr int BLK = 32 * WAVES;
   typedef typename F32Vec<DC>::T VecC;
   // the current query tile's q~ and dO rows, shared by the four waves
   __shared__ __attribute__((aligned(16))) float ql[32][QP];
@@ -95,7 +100,7 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const Bw
   const int gsi = (int)(blockIdx.x / nbh) % p.g_split;
   const int bh = (int)(blockIdx.x % nbh);
   const int b = bh / p.Hkv, hk = bh % p.Hkv;
-  const int kw0 = kb * kBwdF32Block;  // first key of the workgroup
+  const int kw0 = kb * BLK;  // first key of the workgroup
   const int gpw = p.G / p.g_split;
   const int k0 = kw0 + w * 32;
 
@@ -108,12 +113,21 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const Bw
     q_lo = kw0;
   } else if (mask == MASK_SW) {
     q_lo = max(0, kw0 - p.window + 1);
-    q_hi = min(q_hi, kw0 + kBwdF32Block - 1 + p.window);
+    q_hi = min(q_hi, kw0 + BLK - 1 + p.window);
   } else if (mask == MASK_CSW) {
     q_lo = kw0;
-    q_hi = min(q_hi, kw0 + kBwdF32Block - 1 + p.window);
+    q_hi = min(q_hi, kw0 + BLK - 1 + p.window);
   }
   q_lo &= ~31;
+  // query tiles: a range, or the K-major list of this key block (entries of
+  // block_m queries, bs_sub tiles each)
+  int ntq = q_hi > q_lo ? (q_hi - q_lo + 31) / 32 : 0, bs_sub = 1;
+  const int32_t* bs_row = nullptr;
+  if (mask == MASK_BS) {
+    bs_sub = p.bs_block_m / 32;
+    bs_row = p.bs_q_idx + kb * p.bs_q_rs;
+    ntq = p.bs_q_num[kb] * bs_sub;
+  }
 
   const float zc = p.scale * kLog2e;
   const int key = k0 + col;  // this lane's key in S and dP
@@ -134,9 +148,11 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dkv_f32_kernel(const Bw
     const float* qt = reinterpret_cast<const float*>(p.qt) + b * p.qts[0] + hq * p.qts[1];
     const float* dog = reinterpret_cast<const float*>(p.dout) + b * p.dos[0] + hq * p.dos[1];
     const float* ld = p.ld + 2 * ((int64_t)(b * p.Hq + hq) * p.Nq);
-    for (int q0 = q_lo; q0 < q_hi; q0 += 32) {
+    for (int t = 0; t < ntq; ++t) {
+      const int q0 = mask == MASK_BS ? bs_row_get(bs_row, ntq, bs_row, t / bs_sub) * p.bs_block_m + (t % bs_sub) * 32
+                                     : q_lo + 32 * t;
       __syncthreads();  // every wave is done with the previous tile
-      for (int idx = threadIdx.x; idx < 32 * (D / 4); idx += kBwdF32Waves * 64) {
+      for (int idx = threadIdx.x; idx < 32 * (D / 4); idx += WAVES * 64) {
         const int r = idx / (D / 4), c4 = (idx % (D / 4)) * 4;
         const int n = q0 + r;
         f32x4 a = {0.f, 0.f, 0.f, 0.f}, g = {0.f, 0.f, 0.f, 0.f};
@@ -283,10 +299,10 @@ __global__ void __launch_bounds__(256) bwd_dkv_combine_f32_kernel(const BwdParam
                             d) = sv;
 }
 
-template <int D>
-__global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dq_f32_kernel(const BwdParams p, int mask, int bias,
-                                                                        int rope) {
+template <int D, int WAVES = kBwdF32Waves>
+__global__ void __launch_bounds__(WAVES * 64) bwd_dq_f32_kernel(const BwdParams p, int mask, int bias, int rope) {
   constexpr int DH = D / 2, DC = D / 32, KP = D + 4;
+  constexpr int BLK = 32 * WAVES;
   typedef typename F32Vec<DC>::T VecC;
   // the current key tile's k~ and v rows, shared by the four waves
   __shared__ __attribute__((aligned(16))) float kl[32][KP];
@@ -299,7 +315,7 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dq_f32_kernel(const Bwd
   const int bh = (int)(blockIdx.x % nbh);
   if (mask == MASK_CAUSAL || mask == MASK_CSW) mb = p.n_qblocks - 1 - mb;
   const int b = bh / p.Hq, hq = bh % p.Hq, hk = hq / p.G;
-  const int qw0 = mb * kBwdF32Block;  // first query of the workgroup
+  const int qw0 = mb * BLK;  // first query of the workgroup
   const int q0 = qw0 + w * 32;
   const int qrow = q0 + col;
   const int qc = min(qrow, p.Nq - 1);  // clamped: rows >= N_q compute, store nothing
@@ -319,15 +335,27 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dq_f32_kernel(const Bwd
   // loop and reaches every barrier.
   int n_lo = 0, n_hi = p.Nkv;
   if (mask == MASK_CAUSAL) {
-    n_hi = min(n_hi, qw0 + kBwdF32Block);
+    n_hi = min(n_hi, qw0 + BLK);
   } else if (mask == MASK_SW) {
     n_lo = max(0, qw0 - p.window + 1);
-    n_hi = min(n_hi, qw0 + kBwdF32Block - 1 + p.window);
+    n_hi = min(n_hi, qw0 + BLK - 1 + p.window);
   } else if (mask == MASK_CSW) {
     n_lo = max(0, qw0 - p.window + 1);
-    n_hi = min(n_hi, qw0 + kBwdF32Block);
+    n_hi = min(n_hi, qw0 + BLK);
   }
   n_lo &= ~31;
+  // key tiles: a range, or the Q-major lists of this query block (full, then
+  // partial; entries of block_n keys, bs_sub tiles each)
+  int ntk = n_hi > n_lo ? (n_hi - n_lo + 31) / 32 : 0, bs_sub = 1, bs_nfull = 0;
+  const int32_t* bs_full = nullptr;
+  const int32_t* bs_part = nullptr;
+  if (mask == MASK_BS) {
+    bs_sub = p.bs_block_n / 32;
+    bs_nfull = p.bs_full_num[mb];
+    bs_full = p.bs_full_idx + mb * p.bs_full_rs;
+    bs_part = p.bs_part_idx + mb * p.bs_part_rs;
+    ntk = (bs_nfull + p.bs_part_num[mb]) * bs_sub;
+  }
 
   const float zc = p.scale * kLog2e;
   const float slope = bias == BIAS_ALIBI ? p.slopes[hq] * kLog2e : 0.f;
@@ -341,9 +369,11 @@ __global__ void __launch_bounds__(kBwdF32Waves * 64) bwd_dq_f32_kernel(const Bwd
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[c][r] = 0.f;
 
-  for (int n0 = n_lo; n0 < n_hi; n0 += 32) {
+  for (int t = 0; t < ntk; ++t) {
+    const int n0 = mask == MASK_BS ? bs_row_get(bs_full, bs_nfull, bs_part, t / bs_sub) * p.bs_block_n + (t % bs_sub) * 32
+                                   : n_lo + 32 * t;
     __syncthreads();  // every wave is done with the previous tile
-    for (int idx = threadIdx.x; idx < 32 * (D / 4); idx += kBwdF32Waves * 64) {
+    for (int idx = threadIdx.x; idx < 32 * (D / 4); idx += WAVES * 64) {
       const int r = idx / (D / 4), c4 = (idx % (D / 4)) * 4;
       const int n = n0 + r;
       f32x4 a = {0.f, 0.f, 0.f, 0.f}, v = {0.f, 0.f, 0.f, 0.f};

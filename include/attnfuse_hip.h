@@ -66,7 +66,7 @@ typedef enum af_norm { AF_NORM_SOFTMAX = 0, AF_NORM_RELU = 1 } af_norm;
 /* Specialisation key: replaces the reference's Triton constexpr record
  * (attnfuse/compiler/codegen.py:391-404; attnfuse/ir/tiled.py:52-81). */
 typedef struct af_spec_key {
-  int32_t dtype;     /* af_dtype; AF_F32: every entry point except the block-sparse backward */
+  int32_t dtype;     /* af_dtype; AF_F32: every entry point, head dims 32/64/128 */
   int32_t head_dim;  /* instantiated: 32, 64, 128, 256 (256: fp16/bf16 only; af_query) */
   int32_t mask;      /* af_mask                   */
   int32_t bias;      /* af_bias                   */
@@ -244,8 +244,9 @@ typedef struct af_bwd_args {
  * (grids of at most two workgroups per CU), fp32 dK and dV partial sums
  * per split. */
 size_t af_bwd_workspace_bytes(const af_bwd_args* args);
-/* fp16 / bf16, or AF_F32 (fp32 throughout on the fp32 MFMAs; dense, causal
- * and windowed masks only, bm must then be NULL). */
+/* fp16 / bf16, or AF_F32 (fp32 throughout on the fp32 MFMAs, head dims 32,
+ * 64, 128).  Block-sparse (key.mask AF_MASK_BLOCK_SPARSE) needs bm with
+ * BLOCK_M and BLOCK_N of 64 or 128. */
 int af_bwd(const af_bwd_args* args, const af_blockmask* bm /* nullable */,
            void* workspace, size_t workspace_bytes, void* stream);
 /* Workspace bytes af_bwd needs with this block mask (nullable): the above

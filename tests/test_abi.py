@@ -78,9 +78,9 @@ def test_query_and_tile():
 
 
 def test_fp32_coverage_of_the_entry_points():
-    """fp32 has forward (block-sparse included), decode and backward kernels;
-    the block-sparse backward and head dim 256 refuse it with a message, and
-    decode without a workspace fails on the workspace, not the dtype."""
+    """fp32 has forward and backward (block-sparse included) and decode
+    kernels; head dim 256 refuses it with a message, and decode without a
+    workspace fails on the workspace, not the dtype."""
     lib = N.lib()
     assert lib.af_query(N.SpecKeyC(2, 64, 3, 0, 0, 0)) == 1      # fp32 block-sparse forward
     assert lib.af_query(N.SpecKeyC(2, 256, 0, 0, 0, 0)) == 0     # fp32 head dim 256
@@ -96,9 +96,11 @@ def test_fp32_coverage_of_the_entry_points():
     assert lib.af_decode(a, None, 0, None) == N.AF_ERR_UNSUPPORTED
     assert "256" in N.last_error()
     b = N.BwdArgsC()
-    b.key = N.SpecKeyC(2, 64, 3, 0, 0, 0)
+    b.key = N.SpecKeyC(2, 256, 3, 0, 0, 0)
     assert lib.af_bwd(b, None, None, 0, None) == N.AF_ERR_UNSUPPORTED
-    assert "fp16 or bf16" in N.last_error()
+    assert "32, 64 and 128" in N.last_error()
+    b.key = N.SpecKeyC(2, 64, 3, 0, 0, 0)          # fp32 block-sparse: checked further on
+    assert lib.af_bwd(b, None, None, 0, None) == N.AF_ERR_BAD_ARG
 
 
 def test_argument_errors_need_no_gpu():

@@ -4,8 +4,9 @@ The reference runs fp32 backward in TF32 with dQ's product cast to bf16 and
 tests it at 2e-2 (tests/test_backward.py:30-33,63-106).  Here every product
 is fp32, so the bound is ||g - g_ref||_F / ||g_ref||_F <= 1e-4 per gradient
 and 3e-5 max-abs on O.  Cases mirror the 16-bit backward tests: every mask,
-ALiBi, fused RoPE, ragged lengths, head dims 32/64/128, GQA group sums and
-an empty side.
+ALiBi, fused RoPE, ragged lengths, head dims 32/64/128, GQA group sums,
+an empty side, and block masks (64/128 blocks, the workgroup walking its
+block's K-major or Q-major list).
 """
 import pytest
 import torch
@@ -119,3 +120,70 @@ def test_backward_deterministic():
     torch.cuda.synchronize()
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+BS_PATTERNS = {
+    "bigbird": lambda q, k: ((q // 64) == 0) | ((k // 64) == 0) | (((q // 64) - (k // 64)).abs() <= 1),
+    "strided": lambda q, k: ((q // 64) + (k // 64)) % 2 == 0,
+    "local": lambda q, k: ((q // 64) - (k // 64)).abs() <= 1,
+}
+
+
+def run_bs(grid, bmq, bnk, B, Hq, Hkv, N, D, *, rope=False, alibi=False, seed=0):
+    from attnfuse.runtime.block_mask import (block_mask_from_blocks, run_block_sparse,
+                                             run_block_sparse_backward)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    Q, dO = (torch.randn(B, Hq, N, D, generator=g, device="cuda", dtype=F32) for _ in range(2))
+    K, V = (torch.randn(B, Hkv, N, D, generator=g, device="cuda", dtype=F32) for _ in range(2))
+    kw, okw = {}, {}
+    if rope:
+        cos, sin = build_rope_cache(N, D, device="cuda", dtype=F32)
+        kw.update(cos=cos, sin=sin)
+        okw["rope"] = (cos[0, 0].cpu(), sin[0, 0].cpu())
+    if alibi:
+        slopes = torch.tensor(O.alibi_slopes(Hq), dtype=F32, device="cuda")
+        kw["alibi_slopes"] = slopes
+        okw["alibi_slopes"] = slopes.cpu().double()
+    bm = block_mask_from_blocks(grid, bmq, bnk, device="cuda")
+    lse = torch.empty(B, Hq, N, device="cuda", dtype=F32)
+    bias = 1 if alibi else 0
+    out = run_block_sparse(Q, K, V, bm, D ** -0.5, bias_kind=bias, save_lse=lse, **kw)
+    dq, dk, dv = run_block_sparse_backward(Q, K, V, out, lse, dO, bm, D ** -0.5, bias_kind=bias, **kw)
+    torch.cuda.synchronize()
+    em = O.element_mask_from_grid(grid, N, N, bmq, bnk)
+    o_ref, rq, rk, rv = O.attention_grads(Q.cpu(), K.cpu(), V.cpu(), dO.cpu(), dtype=torch.float64, elem_mask=em,
+                                          **okw)
+    errs = {"O": (out.double().cpu() - o_ref).abs().max().item(),
+            "dQ": rel(dq.double(), rq), "dK": rel(dk.double(), rk), "dV": rel(dv.double(), rv)}
+    assert errs["O"] <= FWD_TOL, errs
+    for t in ("dQ", "dK", "dV"):
+        assert errs[t] <= GRAD_REL, errs
+
+
+@pytest.mark.parametrize("blocks", [(64, 64), (128, 64), (64, 128), (128, 128)])
+@pytest.mark.parametrize("name", sorted(BS_PATTERNS))
+def test_block_sparse_backward(name, blocks):
+    """fp32 gradients with a BlockMask: dK/dV workgroups of block_n / 32
+    waves walk their key block's K-major list, dQ workgroups their query
+    block's Q-major lists."""
+    print(f"[bwd f32] block-sparse {name} {blocks}", flush=True)
+    bmq, bnk = blocks
+    N = 384
+    grid = O.block_grid(BS_PATTERNS[name], N, N, bmq, bnk)
+    run_bs(grid, bmq, bnk, 2, 4, 4, N, 64, seed=21)
+
+
+@pytest.mark.parametrize("split", [0, 2])
+def test_block_sparse_backward_gqa_rope_alibi(split, monkeypatch):
+    """GQA (4 query heads on 2 KV heads) with RoPE and ALiBi and a block
+    row with no block at all, under the library's and an explicit group
+    split; head dims 32 and 128."""
+    from attentionfuse_amd.runtime import backward as bwd
+    monkeypatch.setitem(bwd._BWD_TILE, "auto", split == 0)
+    monkeypatch.setitem(bwd._BWD_TILE, "group_split", split)
+    for D in (32, 128):
+        print(f"[bwd f32] block-sparse gqa split={split} D={D}", flush=True)
+        N = 320
+        grid = O.block_grid(BS_PATTERNS["bigbird"], N, N, 64, 64)
+        grid[3, :] = False
+        run_bs(grid, 64, 64, 1, 4, 2, N, D, rope=True, alibi=True, seed=22)
