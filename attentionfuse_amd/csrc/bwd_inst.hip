@@ -25,13 +25,25 @@ namespace {
 template <int MASK, int BIAS, bool ROPE, int WK, int WQ>
 void go(const BwdParams& p, const BwdGrids& g, hipStream_t s) {
   hipLaunchKernelGGL((bwd_prep_kernel<Elem, AF_D, ROPE>), dim3(g.prep), dim3(256), 0, s, p);
-  // at head dim 256 the ALiBi dK/dV kernels crash the compiler's backend
-  // with MFMAs forced into the VGPR form; they are built in bwd_d256_alt.hip
-  if constexpr (AF_D == 256 && BIAS == BIAS_ALIBI)
+  if constexpr (AF_D == 256 && BIAS == BIAS_ALIBI) {
+    // at head dim 256 the ALiBi dK/dV kernels crash the compiler's backend
+    // with MFMAs forced into the VGPR form; they are built in
+    // bwd_d256_alt.hip, and run as their own launch
     launch_bwd_dkv_d256_alibi(p, AF_DT, MASK, ROPE, WK, dim3(g.dkv), s);
-  else
+    hipLaunchKernelGGL((bwd_dq_kernel<Elem, AF_D, MASK, BIAS, ROPE, WQ>), dim3(g.dq), dim3(64 * WQ), 0, s, p);
+  } else if constexpr (WK == WQ && !(AF_D == 128 && BIAS == BIAS_ALIBI)) {
+    // dK/dV and dQ in one launch, dK/dV workgroups first.  Not with ALiBi at
+    // head dim 128: the dQ side then needs more than the 256 registers of
+    // two waves per SIMD, at which the dK/dV side runs alone (fused at two
+    // waves it spills 40-54 registers).
+    BwdParams q = p;
+    q.n_dkv_wg = (int32_t)g.dkv;
+    hipLaunchKernelGGL((bwd_dkvdq_kernel<Elem, AF_D, MASK, BIAS, ROPE, WK>), dim3(g.dkv + g.dq), dim3(64 * WK), 0,
+                       s, q);
+  } else {
     hipLaunchKernelGGL((bwd_dkv_kernel<Elem, AF_D, MASK, BIAS, ROPE, WK>), dim3(g.dkv), dim3(64 * WK), 0, s, p);
-  hipLaunchKernelGGL((bwd_dq_kernel<Elem, AF_D, MASK, BIAS, ROPE, WQ>), dim3(g.dq), dim3(64 * WQ), 0, s, p);
+    hipLaunchKernelGGL((bwd_dq_kernel<Elem, AF_D, MASK, BIAS, ROPE, WQ>), dim3(g.dq), dim3(64 * WQ), 0, s, p);
+  }
   if (g.combine > 0)
     hipLaunchKernelGGL((bwd_dkv_combine_kernel<Elem, AF_D, ROPE>), dim3(g.combine), dim3(256), 0, s, p);
 }

@@ -99,6 +99,8 @@ struct BwdParams {
   float* part_dq;
   float* part_dk;
   float* part_dv;
+  // bwd_dkvdq_kernel: workgroups [0, n_dkv_wg) run dK/dV, the rest dQ
+  int32_t n_dkv_wg;
   float scale;
 };
 
@@ -313,22 +315,30 @@ constexpr int bwd_dkv_waves_per_eu() {
   return D <= 64 ? 3 : 1;
 }
 
+// LDS of a dK/dV workgroup (16-bit elements): NS stages of the q~ tile, the
+// dO tile and 32 (L log2 e, delta) pairs, and for D > 64 the V block.  The
+// loads of stage t + NS - 1 are issued while stage t computes.  Head dims
+// from 128 on keep two stages: with the V block a third would leave room for
+// one 4-wave workgroup per CU (D = 128), or none (D = 256).
+template <int D, int WAVES>
+struct DkvLds {
+  static constexpr int TILE = 32 * D;
+  static constexpr int STAGE = 2 * TILE + 128;
+  static constexpr int VBLK = D > 64 ? 32 * WAVES * D : 0;
+  static constexpr int NS = D >= 128 ? 2 : 3;
+  static constexpr int ELEMS = NS * STAGE + VBLK;
+};
+
+// One dK/dV workgroup, index wg of the dK/dV grid, with its LDS at lds.
 template <class E, int D, int MASK, int BIAS, bool ROPE, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(bwd_dkv_waves_per_eu<D>())))
-    bwd_dkv_kernel(const BwdParams p) {
+__device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, int wg) {
   constexpr int NT = WAVES * 64;
   constexpr int BK = 32 * WAVES;
   constexpr int KS = D / 16, DB = D / 32;
   constexpr bool VLDS = D > 64;            // V block in LDS instead of registers
-  constexpr int TILE = 32 * D;             // one 32-row tile (elements)
-  constexpr int STAGE = 2 * TILE + 128;    // q~ tile, dO tile, 32 (L log2 e, delta) pairs
-  constexpr int VBLK = VLDS ? BK * D : 0;
-  // stages in LDS: the loads of stage t + NS - 1 are issued while stage t
-  // computes.  Head dims from 128 on keep two: with the V block a third
-  // would leave room for one 4-wave workgroup per CU (D = 128), or none
-  // (D = 256).
-  constexpr int NS = D >= 128 ? 2 : 3;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[NS * STAGE + VBLK];
+  constexpr int TILE = DkvLds<D, WAVES>::TILE;    // one 32-row tile (elements)
+  constexpr int STAGE = DkvLds<D, WAVES>::STAGE;
+  constexpr int NS = DkvLds<D, WAVES>::NS;
 
   // no keys: nothing to write (the launch still has one workgroup)
   if (p.n_kblocks <= 0) return;
@@ -340,8 +350,8 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // most query tiles, so they are dispatched first.  Then the head-group
   // split, then (batch, key/value head).
   const int BHK = p.B * p.Hkv;
-  const int kbi = blockIdx.x / (BHK * p.g_split);
-  const int rem = blockIdx.x - kbi * (BHK * p.g_split);
+  const int kbi = wg / (BHK * p.g_split);
+  const int rem = wg - kbi * (BHK * p.g_split);
   // block-sparse plan item: a piece [e0, e0 + ne) of column kb's list
   int kb = kbi, bs_e0 = 0, bs_ne = -1, bs_slot = -1;
   if constexpr (MASK == MASK_BS) {
@@ -613,16 +623,25 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
 // ---------------------------------------------------------------------------
 // dQ
 // ---------------------------------------------------------------------------
+// LDS of a dQ workgroup (16-bit elements): three stages of the k~ and v
+// tiles; the loads of stage t + 2 are issued while stage t computes.
+template <int D>
+struct DqLds {
+  static constexpr int TILE = 32 * D;
+  static constexpr int STAGE = 2 * TILE;
+  static constexpr int NS = 3;
+  static constexpr int ELEMS = NS * STAGE;
+};
+
+// One dQ workgroup, index wg of the dQ grid, with its LDS at lds.
 template <class E, int D, int MASK, int BIAS, bool ROPE, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
+__device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, int wg) {
   constexpr int NT = WAVES * 64;
   constexpr int BMq = 32 * WAVES;
   constexpr int KS = D / 16, DB = D / 32;
-  constexpr int TILE = 32 * D;
-  constexpr int STAGE = 2 * TILE;   // k~ tile, v tile
-  // stages in LDS: the loads of stage t + 2 are issued while stage t computes
-  constexpr int NS = 3;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[NS * STAGE];
+  constexpr int TILE = DqLds<D>::TILE;
+  constexpr int STAGE = DqLds<D>::STAGE;
+  constexpr int NS = DqLds<D>::NS;
 
   // no queries: nothing to write (the launch still has one workgroup)
   if (p.n_qblocks <= 0) return;
@@ -631,8 +650,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int BH = p.B * p.Hq;
-  const int bh = blockIdx.x % BH;
-  const int mbi = blockIdx.x / BH;
+  const int bh = wg % BH;
+  const int mbi = wg / BH;
   const bool heavy_last = MASK == MASK_CAUSAL || MASK == MASK_CSW;
   // block-sparse plan item: a piece [e0, e0 + ne) of row mb's list
   int mb = heavy_last ? (p.n_qblocks - 1 - mbi) : mbi;
@@ -812,6 +831,38 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
   }
   store_grad_rows<E, D, ROPE>(dq, p.dq + b * p.dqs[0] + hq * p.dqs[1], p.dqs[2], qrow, p.Nq, p.scale, p.cos,
                               p.sin, p.rs[0], h);
+}
+
+// ---------------------------------------------------------------------------
+// Kernels
+// ---------------------------------------------------------------------------
+template <class E, int D, int MASK, int BIAS, bool ROPE, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(bwd_dkv_waves_per_eu<D>())))
+    bwd_dkv_kernel(const BwdParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[DkvLds<D, WAVES>::ELEMS];
+  bwd_dkv_body<E, D, MASK, BIAS, ROPE, WAVES>(p, lds, blockIdx.x);
+}
+
+template <class E, int D, int MASK, int BIAS, bool ROPE, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64) bwd_dq_kernel(const BwdParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[DqLds<D>::ELEMS];
+  bwd_dq_body<E, D, MASK, BIAS, ROPE, WAVES>(p, lds, blockIdx.x);
+}
+
+// dK/dV and dQ in one launch: workgroups [0, n_dkv_wg) are the dK/dV grid,
+// the rest the dQ grid.  Both read only the prep kernel's output, and the
+// dispatcher starts workgroups in index order, so dQ workgroups take the
+// slots that short dK/dV workgroups free (under a causal mask the first key
+// blocks walk every query tile and the last almost none).
+template <class E, int D, int MASK, int BIAS, bool ROPE, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(bwd_dkv_waves_per_eu<D>())))
+    bwd_dkvdq_kernel(const BwdParams p) {
+  constexpr int EK = DkvLds<D, WAVES>::ELEMS, EQ = DqLds<D>::ELEMS;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[EK > EQ ? EK : EQ];
+  if ((int)blockIdx.x < p.n_dkv_wg)
+    bwd_dkv_body<E, D, MASK, BIAS, ROPE, WAVES>(p, lds, blockIdx.x);
+  else
+    bwd_dq_body<E, D, MASK, BIAS, ROPE, WAVES>(p, lds, (int)blockIdx.x - p.n_dkv_wg);
 }
 
 }  // namespace af
