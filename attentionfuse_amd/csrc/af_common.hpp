@@ -520,20 +520,29 @@ __device__ inline int bs_row_get(const int32_t* a, int na, const int32_t* b, int
 // tiles per block first.  Tile t of the walk is sub-tile t % sub of entry
 // e0 + t / sub (entries of `blk` rows or keys, sub-tiles of `tile`); tiles
 // from 64 on (walks longer than a work plan's pieces) are looked up in the
-// lists.
+// lists.  Bit 0 of a start (tile starts are multiples of 32) marks a tile of
+// a partial block whose element mask applies.
 struct BsTiles {
-  int lo;
+  int lo;             // lane l: start of tile l, + 1 if it is a masked partial tile
   const int32_t* a;
   const int32_t* b;
+  const int32_t* flags;
   int na, e0, sub, blk, tile;
+  int pmode;          // 0: no element masks; 1: entries >= na (list b) are
+                      // partial; 2: entries e with flags[e] != 0 are
 
-  __device__ int lookup(int t) const {
+  __device__ bool part_of(int e) const {
+    if (pmode == 1) return e >= na;
+    if (pmode == 2) return ((const_i32_ptr)flags)[e] != 0;
+    return false;
+  }
+  __device__ int raw_lookup(int t) const {
     const int e = t / sub;
-    return bs_row_get(a, na, b, e0 + e) * blk + (t - e * sub) * tile;
+    return bs_row_get(a, na, b, e0 + e) * blk + (t - e * sub) * tile + (part_of(e0 + e) ? 1 : 0);
   }
   // lanes past the walk's last tile hold 0 and read no list entry
   __device__ void init(const int32_t* a_, int na_, const int32_t* b_, int e0_, int sub_, int blk_, int tile_,
-                       int ntiles, int lane) {
+                       int ntiles, int lane, int pmode_ = 0, const int32_t* flags_ = nullptr) {
     a = a_;
     na = na_;
     b = b_;
@@ -541,17 +550,26 @@ struct BsTiles {
     sub = sub_;
     blk = blk_;
     tile = tile_;
+    pmode = pmode_;
+    flags = flags_;
     auto at = [&](int t) -> int {
       if (t >= ntiles) return 0;
       const int e = e0 + t / sub;
-      return (e < na ? a[e] : b[e - na]) * blk + (t % sub) * tile;
+      return (e < na ? a[e] : b[e - na]) * blk + (t % sub) * tile + (part_of(e) ? 1 : 0);
     };
     lo = at(lane);
   }
-  __device__ __forceinline__ int operator()(int t) const {
+  __device__ __forceinline__ int raw(int t) const {
     if (t < 64) return __builtin_amdgcn_readlane(lo, t);
-    return lookup(t);
+    return raw_lookup(t);
   }
+  // first row (key or query) of tile t
+  __device__ __forceinline__ int operator()(int t) const { return raw(t) & ~1; }
+  // whether tile t is part of a partial tile whose element bits apply
+  __device__ __forceinline__ bool partial(int t) const { return (raw(t) & 1) != 0; }
+  // list entry of tile t, and its sub-tile within that entry's block
+  __device__ __forceinline__ int entry(int t) const { return e0 + t / sub; }
+  __device__ __forceinline__ int sub_of(int t) const { return t - (t / sub) * sub; }
 };
 
 }  // namespace af

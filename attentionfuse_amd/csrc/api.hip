@@ -222,22 +222,24 @@ int dispatch_fwd(FwdParams p, const af_fwd_args& a, int waves, void* workspace, 
   const dim3 grid((unsigned)p.n_mblocks * (unsigned)(p.B * p.Hq));
   rc = -1;
   const bool f16 = k.dtype == AF_F16;
+  // block-sparse walks with element masks run their own instantiations
+  const int mask = k.mask == AF_MASK_BLOCK_SPARSE && p.bs_row_bits != nullptr ? MASK_BSE : k.mask;
   switch (k.head_dim) {
     case 32:
-      rc = f16 ? launch_fwd_f16_d32(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s)
-               : launch_fwd_bf16_d32(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s);
+      rc = f16 ? launch_fwd_f16_d32(p, mask, k.bias, k.norm, k.rope, waves, grid, s)
+               : launch_fwd_bf16_d32(p, mask, k.bias, k.norm, k.rope, waves, grid, s);
       break;
     case 64:
-      rc = f16 ? launch_fwd_f16_d64(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s)
-               : launch_fwd_bf16_d64(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s);
+      rc = f16 ? launch_fwd_f16_d64(p, mask, k.bias, k.norm, k.rope, waves, grid, s)
+               : launch_fwd_bf16_d64(p, mask, k.bias, k.norm, k.rope, waves, grid, s);
       break;
     case 128:
-      rc = f16 ? launch_fwd_f16_d128(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s)
-               : launch_fwd_bf16_d128(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s);
+      rc = f16 ? launch_fwd_f16_d128(p, mask, k.bias, k.norm, k.rope, waves, grid, s)
+               : launch_fwd_bf16_d128(p, mask, k.bias, k.norm, k.rope, waves, grid, s);
       break;
     case 256:
-      rc = f16 ? launch_fwd_f16_d256(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s)
-               : launch_fwd_bf16_d256(p, k.mask, k.bias, k.norm, k.rope, waves, grid, s);
+      rc = f16 ? launch_fwd_f16_d256(p, mask, k.bias, k.norm, k.rope, waves, grid, s)
+               : launch_fwd_bf16_d256(p, mask, k.bias, k.norm, k.rope, waves, grid, s);
       break;
   }
   if (rc != 0) return fail(AF_ERR_UNSUPPORTED, "no forward instantiation for this key");
@@ -264,6 +266,7 @@ int dispatch_fwd_f32(const af_fwd_args& a, void* workspace, size_t workspace_byt
     q.bs_part_idx = bm->kv_indices;
     q.bs_full_rs = bm->full_kv_stride;
     q.bs_part_rs = bm->kv_stride;
+    q.bs_row_bits = bm->part_row_bits;
   }
   fp.mask = a.key.mask;
   fp.bias = a.key.bias;
@@ -445,6 +448,7 @@ int af_fwd_blocksparse(const af_fwd_args* a, const af_blockmask* bm, void* works
       bm->n_kv_blocks != (a->seqlen_kv + bm->block_n - 1) / bm->block_n)
     return fail(AF_ERR_BAD_ARG, "block mask grid %dx%d does not match sequence lengths %d/%d", bm->n_q_blocks,
                 bm->n_kv_blocks, a->seqlen_q, a->seqlen_kv);
+  if ((rc = check_elem_masks(bm, a->key.head_dim))) return rc;
   if (a->seqlen_q == 0) return AF_OK;
   if (f32) {
     if (a->coverage != nullptr)
@@ -460,6 +464,7 @@ int af_fwd_blocksparse(const af_fwd_args* a, const af_blockmask* bm, void* works
   p.bs_full_rs = bm->full_kv_stride;
   p.bs_part_rs = bm->kv_stride;
   p.bs_block_n = bm->block_n;
+  p.bs_row_bits = bm->part_row_bits;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const BsFwdWorkspace wl = bs_fwd_workspace(*a, bm);
   const bool split = bm->q_items != nullptr && bm->n_q_splits > 0;

@@ -251,6 +251,7 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
     if (bm->n_q_blocks != (a->seqlen_q + bm->block_m - 1) / bm->block_m ||
         bm->n_kv_blocks != (a->seqlen_kv + bm->block_n - 1) / bm->block_n)
       return bad(AF_ERR_BAD_ARG, "block mask grid does not match the sequence lengths");
+    if (const int rc = check_elem_masks(bm, k.head_dim)) return rc;
     g.waves_kv = bm->block_n / 32;
     g.waves_q = bm->block_m / 32;
     p.bs_full_num = bm->full_kv_num;
@@ -262,6 +263,9 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
     p.bs_full_rs = bm->full_kv_stride;
     p.bs_part_rs = bm->kv_stride;
     p.bs_q_rs = bm->q_stride;
+    p.bs_row_bits = bm->part_row_bits;
+    p.bs_col_bits = bm->q_col_bits;
+    p.bs_q_partial = bm->q_partial;
     p.bs_block_m = bm->block_m;
     p.bs_block_n = bm->block_n;
     if (wl.q_plan) {
@@ -305,23 +309,25 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   }
 
   const bool f16 = k.dtype == AF_F16;
+  // block-sparse walks with element masks run their own instantiations
+  const int mask = k.mask == AF_MASK_BLOCK_SPARSE && p.bs_row_bits != nullptr ? MASK_BSE : k.mask;
   int r = -1;
   switch (k.head_dim) {
     case 32:
-      r = f16 ? launch_bwd_f16_d32(p, k.mask, k.bias, k.rope, g, stream)
-              : launch_bwd_bf16_d32(p, k.mask, k.bias, k.rope, g, stream);
+      r = f16 ? launch_bwd_f16_d32(p, mask, k.bias, k.rope, g, stream)
+              : launch_bwd_bf16_d32(p, mask, k.bias, k.rope, g, stream);
       break;
     case 64:
-      r = f16 ? launch_bwd_f16_d64(p, k.mask, k.bias, k.rope, g, stream)
-              : launch_bwd_bf16_d64(p, k.mask, k.bias, k.rope, g, stream);
+      r = f16 ? launch_bwd_f16_d64(p, mask, k.bias, k.rope, g, stream)
+              : launch_bwd_bf16_d64(p, mask, k.bias, k.rope, g, stream);
       break;
     case 128:
-      r = f16 ? launch_bwd_f16_d128(p, k.mask, k.bias, k.rope, g, stream)
-              : launch_bwd_bf16_d128(p, k.mask, k.bias, k.rope, g, stream);
+      r = f16 ? launch_bwd_f16_d128(p, mask, k.bias, k.rope, g, stream)
+              : launch_bwd_bf16_d128(p, mask, k.bias, k.rope, g, stream);
       break;
     case 256:
-      r = f16 ? launch_bwd_f16_d256(p, k.mask, k.bias, k.rope, g, stream)
-              : launch_bwd_bf16_d256(p, k.mask, k.bias, k.rope, g, stream);
+      r = f16 ? launch_bwd_f16_d256(p, mask, k.bias, k.rope, g, stream)
+              : launch_bwd_bf16_d256(p, mask, k.bias, k.rope, g, stream);
       break;
   }
   if (r != 0) return bad(AF_ERR_UNSUPPORTED, "no backward instantiation for this key");

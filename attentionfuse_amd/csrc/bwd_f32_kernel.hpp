@@ -182,6 +182,18 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_f32_kernel(const BwdParams
 #pragma unroll
         for (int e = 0; e < 4; ++e) dp = __builtin_amdgcn_mfma_f32_32x32x2f32(ga4[e], va4[e], dp, 0, 0, 0);
       }
+      // element mask of a partial block-sparse tile: bits of this lane's key
+      // over the tile's 32 queries, shifted by 4 h (constant bit per element)
+      uint32_t ebits = ~0u;
+      if (mask == MASK_BS && p.bs_col_bits != nullptr) {
+        const int e = t / bs_sub;
+        if (p.bs_q_partial[kb * p.bs_q_rs + e] != 0) {
+          const int sb = t - e * bs_sub;
+          const int64_t word = (((int64_t)kb * p.bs_q_rs + e) * p.bs_block_n + (key - kw0)) *
+                                   ((p.bs_block_m + 63) / 64) + (sb >> 1);
+          ebits = key < p.Nkv ? (uint32_t)(p.bs_col_bits[word] >> (32 * (sb & 1))) >> (4 * h) : 0u;
+        }
+      }
       // P and dS of query q0 + 8(r/4) + 4h + (r mod 4), key k0 + col
       float pr[16], ds[16];
 #pragma unroll
@@ -190,7 +202,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dkv_f32_kernel(const BwdParams
         const f32x2 l2 = *reinterpret_cast<const f32x2*>(ld + 2 * min(qi, p.Nq - 1));
         float x = s[r] * zc - l2[0];
         if (bias == BIAS_ALIBI) x -= slope * (float)abs(qi - key);
-        const bool vis = qi < p.Nq && key < p.Nkv && f32_visible(mask, p.window, qi, key);
+        const bool vis = qi < p.Nq && key < p.Nkv && f32_visible(mask, p.window, qi, key) &&
+                         (ebits & (1u << (8 * (r >> 2) + (r & 3))));
         pr[r] = vis ? __builtin_amdgcn_exp2f(x) : 0.f;
         ds[r] = pr[r] * (dp[r] - l2[1]);
       }
@@ -400,6 +413,19 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_f32_kernel(const BwdParams 
 #pragma unroll
       for (int e = 0; e < 4; ++e) dp = __builtin_amdgcn_mfma_f32_32x32x2f32(v4[e], gh[j][e], dp, 0, 0, 0);
     }
+    // element mask of a partial block-sparse tile (partial entries follow
+    // the full ones): bits of this lane's query row over the tile's 32 keys,
+    // shifted by 4 h (constant bit per element)
+    uint32_t ebits = ~0u;
+    if (mask == MASK_BS && p.bs_row_bits != nullptr) {
+      const int e = t / bs_sub;
+      if (e >= bs_nfull) {
+        const int sb = t - e * bs_sub;
+        const int64_t word = (((int64_t)mb * p.bs_part_rs + (e - bs_nfull)) * p.bs_block_m + (qrow - qw0)) *
+                                 (p.bs_block_n / 64) + (sb >> 1);
+        ebits = qrow < p.Nq ? (uint32_t)(p.bs_row_bits[word] >> (32 * (sb & 1))) >> (4 * h) : 0u;
+      }
+    }
     // dS^T of key n0 + 8(r/4) + 4h + (r mod 4), query qrow
     float ds[16];
 #pragma unroll
@@ -407,7 +433,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_f32_kernel(const BwdParams 
       const int kj = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
       float x = s[r] * zc - l2[0];
       if (bias == BIAS_ALIBI) x -= slope * (float)abs(qrow - kj);
-      const bool vis = qrow < p.Nq && kj < p.Nkv && f32_visible(mask, p.window, qrow, kj);
+      const bool vis = qrow < p.Nq && kj < p.Nkv && f32_visible(mask, p.window, qrow, kj) &&
+                       (ebits & (1u << (8 * (r >> 2) + (r & 3))));
       const float pr = vis ? __builtin_amdgcn_exp2f(x) : 0.f;
       ds[r] = pr * (dp[r] - l2[1]);
     }

@@ -50,7 +50,7 @@ void go(const BwdParams& p, const BwdGrids& g, hipStream_t s) {
 
 template <int MASK, int BIAS, bool ROPE>
 int pick_waves(const BwdParams& p, const BwdGrids& g, hipStream_t s) {
-  if constexpr (MASK == MASK_BS) {
+  if constexpr (kIsBs<MASK>) {
     if (g.waves_kv == 2 && g.waves_q == 2) { go<MASK, BIAS, ROPE, 2, 2>(p, g, s); return 0; }
     if (g.waves_kv == 2 && g.waves_q == 4) { go<MASK, BIAS, ROPE, 2, 4>(p, g, s); return 0; }
     if (g.waves_kv == 4 && g.waves_q == 2) { go<MASK, BIAS, ROPE, 4, 2>(p, g, s); return 0; }
@@ -84,6 +84,9 @@ int AF_FN(AF_DT_NAME, AF_D)(const BwdParams& p, int mask, int bias, int rope, co
     case MASK_CAUSAL: return pick_bias<MASK_CAUSAL>(p, bias, rope, g, s);
     case MASK_SW: return pick_bias<MASK_SW>(p, bias, rope, g, s);
     case MASK_BS: return pick_bias<MASK_BS>(p, bias, rope, g, s);
+#if AF_D <= 128
+    case MASK_BSE: return pick_bias<MASK_BSE>(p, bias, rope, g, s);
+#endif
     case MASK_CSW: return pick_bias<MASK_CSW>(p, bias, rope, g, s);
     default: return -1;
   }

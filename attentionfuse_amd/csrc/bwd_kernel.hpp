@@ -74,6 +74,14 @@ struct BwdParams {
   const int32_t* bs_part_idx;
   const int32_t* bs_q_num;
   const int32_t* bs_q_idx;
+  // Element masks of partial tiles (all three NULL, or none): row bits of
+  // the Q-major partial entries, (n_q_blocks, bs_part_rs, BLOCK_M,
+  // BLOCK_N / 64) words over keys; column bits of the K-major entries,
+  // (n_kv_blocks, bs_q_rs, BLOCK_N, ceil(BLOCK_M / 64)) words over queries;
+  // and which K-major entries are partial, (n_kv_blocks, bs_q_rs).
+  const uint64_t* bs_row_bits;
+  const uint64_t* bs_col_bits;
+  const int32_t* bs_q_partial;
   int64_t qs[4], ks[4], vs[4], os[4], dos[4], dqs[4], dks[4], dvs[4], ls[3], rs[2];
   int64_t qts[4], kts[4];  // strides of qt, kt
   int64_t bs_full_rs, bs_part_rs, bs_q_rs;
@@ -354,7 +362,7 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
   const int rem = wg - kbi * (BHK * p.g_split);
   // block-sparse plan item: a piece [e0, e0 + ne) of column kb's list
   int kb = kbi, bs_e0 = 0, bs_ne = -1, bs_slot = -1;
-  if constexpr (MASK == MASK_BS) {
+  if constexpr (kIsBs<MASK>) {
     if (p.bs_kv_items != nullptr) {
       const int32_t* it = p.bs_kv_items + 4 * kbi;
       kb = it[0];
@@ -404,7 +412,7 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
     m_lo = n0 & ~31;
     m_hi = min(n0 + BK - 1 + p.window, p.Nq);
   }
-  if constexpr (MASK == MASK_BS) {
+  if constexpr (kIsBs<MASK>) {
     bs_sub = p.bs_block_m / 32;
     bs_n = p.bs_q_num[kb];
     bs_row = p.bs_q_idx + kb * p.bs_q_rs;
@@ -413,9 +421,12 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
     ntq = m_hi > m_lo ? (m_hi - m_lo + 31) / 32 : 0;
   }
   BsTiles bst;
-  if constexpr (MASK == MASK_BS) bst.init(bs_row, bs_n, bs_row, bs_e0, bs_sub, p.bs_block_m, 32, ntq, lane);
+  if constexpr (kIsBs<MASK>)
+    bst.init(bs_row, bs_n, bs_row, bs_e0, bs_sub, p.bs_block_m, 32, ntq, lane,
+             MASK == MASK_BSE ? 2 : 0,
+             p.bs_q_partial != nullptr ? p.bs_q_partial + kb * p.bs_q_rs : nullptr);
   auto tile_m0 = [&](int t) -> int {
-    if constexpr (MASK == MASK_BS) {
+    if constexpr (kIsBs<MASK>) {
       return bst(t);
     } else {
       return m_lo + 32 * t;
@@ -487,6 +498,17 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
     if (ahead) load_next(slot == 0 ? NS - 1 : slot - 1);
     const int hq = hq0 + gi;
     const int m0 = tile_m0(tl);
+    // a partial block-sparse tile whose element mask applies: its K-major
+    // entry and 32-row sub-tile
+    bool epart = false;
+    int ee = 0, esb = 0;
+    if constexpr (MASK == MASK_BSE) {
+      epart = bst.partial(tl);
+      if (epart) {
+        ee = bst.entry(tl);
+        esb = bst.sub_of(tl);
+      }
+    }
     adv(gi, tl);
     const uint16_t* buf = lds + slot * STAGE;
     const uint16_t* Qs = buf;
@@ -550,6 +572,17 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
           s[r] = visible<MASK>(qi, key, p.Nq, p.Nkv, p.window) ? s[r] : -INFINITY;
         }
       }
+      if constexpr (MASK == MASK_BSE) {
+        if (epart) {
+          // bits of this lane's key over the tile's 32 query rows, shifted
+          // by 8 h once so that every element tests a constant bit
+          const int wc = (p.bs_block_m + 63) / 64;
+          const int64_t word = (((int64_t)kb * p.bs_q_rs + ee) * p.bs_block_n + (key - n0)) * wc + (esb >> 1);
+          const uint32_t bits = key < p.Nkv ? (uint32_t)(p.bs_col_bits[word] >> (32 * (esb & 1))) >> (8 * h) : 0u;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[r] = (bits & (1u << (16 * (r >> 3) + (r & 7)))) ? s[r] : -INFINITY;
+        }
+      }
       u32x4 pp[2], pd[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -599,7 +632,7 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
 
   uint16_t* dkb = p.dk + b * p.dks[0] + hk * p.dks[1];
   uint16_t* dvb = p.dv + b * p.dvs[0] + hk * p.dvs[1];
-  if (MASK == MASK_BS && bs_slot >= 0) {
+  if (kIsBs<MASK> && bs_slot >= 0) {
     // a piece of a split column
     if (key < p.Nkv) {
       const int64_t row = ((int64_t)bs_slot * BHK + bhk) * BK + (key - n0);
@@ -656,7 +689,7 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
   // block-sparse plan item: a piece [e0, e0 + ne) of row mb's list
   int mb = heavy_last ? (p.n_qblocks - 1 - mbi) : mbi;
   int bs_e0 = 0, bs_ne = -1, bs_slot = -1;
-  if constexpr (MASK == MASK_BS) {
+  if constexpr (kIsBs<MASK>) {
     if (p.bs_q_items != nullptr) {
       const int32_t* it = p.bs_q_items + 4 * mbi;
       mb = it[0];
@@ -691,7 +724,7 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
     n_lo = max(m0 - p.window + 1, 0) & ~31;
     n_hi = min(m0 + BMq, p.Nkv);
   }
-  if constexpr (MASK == MASK_BS) {
+  if constexpr (kIsBs<MASK>) {
     bs_sub = p.bs_block_n / 32;
     bs_nfull = p.bs_full_num[mb];
     bs_npart = p.bs_part_num[mb];
@@ -702,10 +735,11 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
     ntiles = n_hi > n_lo ? (n_hi - n_lo + 31) / 32 : 0;
   }
   BsTiles bst;
-  if constexpr (MASK == MASK_BS)
-    bst.init(bs_full_row, bs_nfull, bs_part_row, bs_e0, bs_sub, p.bs_block_n, 32, ntiles, lane);
+  if constexpr (kIsBs<MASK>)
+    bst.init(bs_full_row, bs_nfull, bs_part_row, bs_e0, bs_sub, p.bs_block_n, 32, ntiles, lane,
+             MASK == MASK_BSE ? 1 : 0);
   auto tile_n0 = [&](int t) -> int {
-    if constexpr (MASK == MASK_BS) {
+    if constexpr (kIsBs<MASK>) {
       return bst(t);
     } else {
       return n_lo + 32 * t;
@@ -792,6 +826,19 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
           s[r] = visible<MASK>(qrow, kj, p.Nq, p.Nkv, p.window) ? s[r] : -INFINITY;
         }
       }
+      if constexpr (MASK == MASK_BSE) {
+        if (bst.partial(t)) {
+          // element mask of a partial tile: bits of this lane's query row
+          // over the tile's 32 keys, shifted by 8 h once so that every
+          // element tests a constant bit
+          const int e = bst.entry(t), sb = bst.sub_of(t);
+          const int64_t word = (((int64_t)mb * p.bs_part_rs + (e - bs_nfull)) * p.bs_block_m + (qrow - m0)) *
+                                   (p.bs_block_n / 64) + (sb >> 1);
+          const uint32_t bits = qrow < p.Nq ? (uint32_t)(p.bs_row_bits[word] >> (32 * (sb & 1))) >> (8 * h) : 0u;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[r] = (bits & (1u << (16 * (r >> 3) + (r & 7)))) ? s[r] : -INFINITY;
+        }
+      }
       u32x4 pd[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -824,7 +871,7 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
     slot = slot + 1 == NS ? 0 : slot + 1;
   }
 
-  if (MASK == MASK_BS && bs_slot >= 0) {
+  if (kIsBs<MASK> && bs_slot >= 0) {
     // a piece of a split row
     if (qrow < p.Nq) store_partial_row<D>(dq, p.part_dq + (((int64_t)bs_slot * BH + bh) * BMq + (qrow - m0)) * D, h);
     return;

@@ -138,11 +138,11 @@ __global__ void __launch_bounds__(kF32Waves * 64) fwd_f32_kernel(const FwdF32Par
   // 32-key tiles: a range, or with a block mask the tiles of the listed key
   // blocks of this wave's mask row (32-row waves never straddle two rows)
   int ntiles = n_hi > n_lo ? (n_hi - n_lo + 31) / 32 : 0;
-  int bs_sub = 1, bs_nfull = 0;
+  int bs_sub = 1, bs_nfull = 0, mr = 0;
   const int32_t* bs_full_row = nullptr;
   const int32_t* bs_part_row = nullptr;
   if (mask == MASK_BS) {
-    const int mr = q0 / p.bs_block_m;
+    mr = q0 / p.bs_block_m;
     bs_sub = p.bs_block_n / 32;
     bs_nfull = p.bs_full_num[mr];
     bs_full_row = p.bs_full_idx + mr * p.bs_full_rs;
@@ -203,6 +203,20 @@ __global__ void __launch_bounds__(kF32Waves * 64) fwd_f32_kernel(const FwdF32Par
     }
     if (t + 1 < ntiles) load_k(tile_n0(t + 1));  // next tile (rows clamped, so in bounds)
 
+    // element mask of a partial block-sparse tile: bits of this lane's
+    // query row over the tile's 32 keys (partial entries follow the full
+    // ones), shifted by 4 h so that every element tests a constant bit
+    uint32_t ebits = ~0u;
+    if (mask == MASK_BS && p.bs_row_bits != nullptr) {
+      const int e = t / bs_sub;
+      if (e >= bs_nfull) {
+        const int sb = t - e * bs_sub;
+        const int64_t word =
+            (((int64_t)mr * p.bs_part_rs + (e - bs_nfull)) * p.bs_block_m + (qrow - mr * p.bs_block_m)) *
+                (p.bs_block_n / 64) + (sb >> 1);
+        ebits = qrow < p.Nq ? (uint32_t)(p.bs_row_bits[word] >> (32 * (sb & 1))) >> (4 * h) : 0u;
+      }
+    }
     float x[16];
     float mt = -INFINITY;
 #pragma unroll
@@ -215,6 +229,7 @@ __global__ void __launch_bounds__(kF32Waves * 64) fwd_f32_kernel(const FwdF32Par
       if (mask == MASK_CAUSAL) vis = vis && key <= qrow;
       else if (mask == MASK_SW) vis = vis && abs(qrow - key) < p.window;
       else if (mask == MASK_CSW) vis = vis && key <= qrow && key > qrow - p.window;
+      vis = vis && (ebits & (1u << (8 * (r >> 2) + (r & 3))));
       x[r] = vis ? v : -INFINITY;
       mt = fmaxf(mt, x[r]);
     }

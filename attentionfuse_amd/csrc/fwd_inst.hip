@@ -46,7 +46,7 @@ int go(const FwdParams& p, dim3 grid, hipStream_t s) {
 
 template <int MASK, int BIAS, int NORM, bool ROPE>
 int pick_waves(const FwdParams& p, int waves, dim3 grid, hipStream_t s) {
-  if constexpr (MASK == MASK_BS) {
+  if constexpr (kIsBs<MASK>) {
     switch (waves) {
       case 1: return go<MASK, BIAS, NORM, ROPE, 1>(p, grid, s);
       case 2: return go<MASK, BIAS, NORM, ROPE, 2>(p, grid, s);
@@ -93,6 +93,9 @@ int AF_FN(AF_DT_NAME, AF_D)(const FwdParams& p, int mask, int bias, int norm,
     case MASK_CAUSAL: return pick_bias<MASK_CAUSAL>(p, bias, norm, rope, waves, grid, s);
     case MASK_SW: return pick_bias<MASK_SW>(p, bias, norm, rope, waves, grid, s);
     case MASK_BS: return pick_bias<MASK_BS>(p, bias, norm, rope, waves, grid, s);
+#if AF_D <= 128
+    case MASK_BSE: return pick_bias<MASK_BSE>(p, bias, norm, rope, waves, grid, s);
+#endif
     case MASK_CSW: return pick_bias<MASK_CSW>(p, bias, norm, rope, waves, grid, s);
     default: return -1;
   }

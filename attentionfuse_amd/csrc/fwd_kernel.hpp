@@ -33,7 +33,13 @@
 
 namespace af {
 
-enum { MASK_FULL = 0, MASK_CAUSAL = 1, MASK_SW = 2, MASK_BS = 3, MASK_CSW = 4 };
+// MASK_BSE (no af_mask value of its own): a block-sparse walk whose partial
+// tiles carry element masks (af_blockmask.part_row_bits ...); its kernels
+// are instantiated apart, so that plain block-sparse walks keep no state for
+// them.  Head dims up to 128.
+enum { MASK_FULL = 0, MASK_CAUSAL = 1, MASK_SW = 2, MASK_BS = 3, MASK_CSW = 4, MASK_BSE = 5 };
+template <int MASK>
+inline constexpr bool kIsBs = MASK == MASK_BS || MASK == MASK_BSE;
 enum { BIAS_NONE = 0, BIAS_ALIBI = 1, BIAS_ADD = 2 };
 enum { NORM_SOFTMAX = 0, NORM_RELU = 1 };
 
@@ -57,6 +63,10 @@ struct FwdParams {
   // O to part_o and its (running max, row sum) to part_ml, both indexed
   // (slot, B*Hq, BLOCK_M), for the combine kernel.
   const int32_t* bs_items;
+  // Element masks of the partial tiles (nullable): (n_q_blocks,
+  // bs_part_rs, BLOCK_M, BLOCK_N / 64) words, bit k of word w of row r set
+  // when query r of the block sees key 64 w + k of the entry's key block.
+  const uint64_t* bs_row_bits;
   float* part_o;
   float* part_ml;
   int64_t qs[4], ks[4], vs[4], os[4], ls[3], rs[2], bs[4];
@@ -110,7 +120,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // block-sparse plan item: a piece [e0, e0 + ne) of row mb's list
   int mb = heavy_last ? (p.n_mblocks - 1 - mbi) : mbi;
   int bs_e0 = 0, bs_ne = -1, bs_slot = -1;
-  if constexpr (MASK == MASK_BS) {
+  if constexpr (kIsBs<MASK>) {
     if (p.bs_items != nullptr) {
       const int32_t* it = p.bs_items + 4 * mbi;
       mb = it[0];
@@ -171,7 +181,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     n_lo = max(m0 - p.window + 1, 0) & ~(BN - 1);
     n_hi = min(m0 + BM, p.Nkv);
   }
-  if constexpr (MASK == MASK_BS) {
+  if constexpr (kIsBs<MASK>) {
     bs_sub = p.bs_block_n / BN;
     bs_nfull = p.bs_full_num[mb];
     bs_npart = p.bs_part_num[mb];
@@ -182,10 +192,11 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     ntiles = n_hi > n_lo ? (n_hi - n_lo + BN - 1) / BN : 0;
   }
   BsTiles bst;
-  if constexpr (MASK == MASK_BS)
-    bst.init(bs_full_row, bs_nfull, bs_part_row, bs_e0, bs_sub, p.bs_block_n, BN, ntiles, lane);
+  if constexpr (kIsBs<MASK>)
+    bst.init(bs_full_row, bs_nfull, bs_part_row, bs_e0, bs_sub, p.bs_block_n, BN, ntiles, lane,
+             MASK == MASK_BSE ? 1 : 0);
   auto tile_n0 = [&](int t) -> int {
-    if constexpr (MASK == MASK_BS) {
+    if constexpr (kIsBs<MASK>) {
       return bst(t);
     } else {
       return n_lo + t * BN;
@@ -394,6 +405,27 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
           bool ok = kr <= hi;
           if constexpr (MASK == MASK_SW || MASK == MASK_CSW) ok = ok && kr >= lo;
           s[kb][r] = ok ? s[kb][r] : -INFINITY;
+        }
+      }
+    }
+    if constexpr (MASK == MASK_BSE) {
+      // element mask of a partial block-sparse tile (rare; a uniform
+      // branch): the bits of this lane's query row over the tile's 64 keys,
+      // key block kb in half kb
+      if (bst.partial(t)) {
+        const int e = bst.entry(t);
+        const int64_t word = (((int64_t)mb * p.bs_part_rs + (e - bs_nfull)) * p.bs_block_m + (qrow - m0)) *
+                                 (p.bs_block_n / 64) + bst.sub_of(t);
+        const uint32_t* bits = reinterpret_cast<const uint32_t*>(p.bs_row_bits + word);
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb) {
+          // shifted by this lane's 8 h once, so that every element tests a
+          // constant bit (per-element lane shifts would be hoisted out of the
+          // loop and held in registers)
+          const uint32_t half = (qrow < p.Nq ? bits[kb] : 0u) >> (8 * h);
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            s[kb][r] = (half & (1u << (16 * (r >> 3) + (r & 7)))) ? s[kb][r] : -INFINITY;
         }
       }
     }
@@ -673,7 +705,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // this lane's 32 keys of every tile, plus the partner lane's 32
   float lt = lsum[0] + lsum[1];
   lt += xor32(lt);
-  if (MASK == MASK_BS && bs_slot >= 0) {
+  if (kIsBs<MASK> && bs_slot >= 0) {
     // a piece of a split row: unnormalised O and (m, l) for the combine
     if (qrow < p.Nq) {
       const int64_t prow = ((int64_t)bs_slot * BH + bh) * BM + (qrow - m0);

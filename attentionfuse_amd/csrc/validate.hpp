@@ -47,6 +47,25 @@ inline int check_bhnd(const char* name, const void* ptr, const int64_t* st, int6
   return AF_OK;
 }
 
+// Element masks of a block mask: all three arrays or none, over key blocks of
+// whole 64-bit words, head dims up to 128.
+inline int check_elem_masks(const af_blockmask* bm, int head_dim) {
+  const int n = (bm->part_row_bits != nullptr) + (bm->q_col_bits != nullptr) + (bm->q_partial != nullptr);
+  if (n != 0 && n != 3) {
+    set_error("block mask element masks: part_row_bits, q_col_bits and q_partial must be all NULL or all set");
+    return AF_ERR_BAD_ARG;
+  }
+  if (n == 3 && head_dim > 128) {
+    set_error("block mask element masks: head dims up to 128 (got %d)", head_dim);
+    return AF_ERR_UNSUPPORTED;
+  }
+  if (n == 3 && bm->block_n % 64 != 0) {
+    set_error("block mask element masks need BLOCK_N a multiple of 64 (got %d)", bm->block_n);
+    return AF_ERR_UNSUPPORTED;
+  }
+  return AF_OK;
+}
+
 inline bool head_dim_supported(int d) { return d == 32 || d == 64 || d == 128 || d == 256; }
 
 }  // namespace af

@@ -47,7 +47,9 @@ class BlockMaskC(C.Structure):
                 ("n_q_items", C.c_int32), ("n_q_splits", C.c_int32),
                 ("n_q_slots", C.c_int32),
                 ("n_kv_items", C.c_int32), ("n_kv_splits", C.c_int32),
-                ("n_kv_slots", C.c_int32)]
+                ("n_kv_slots", C.c_int32),
+                ("part_row_bits", C.c_void_p), ("q_col_bits", C.c_void_p),
+                ("q_partial", C.c_void_p)]
 
 
 class FwdArgsC(C.Structure):
@@ -129,7 +131,7 @@ SIGNATURES = {
     "af_abi_version": (C.c_int, []),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib = None
 _lock = threading.Lock()

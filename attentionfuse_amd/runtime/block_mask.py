@@ -10,7 +10,13 @@ active element is rounded up to fully active), a K-major transpose
 
 ``create_block_mask`` evaluates the predicate on the (Q_LEN, KV_LEN) index
 grid exactly like the reference, but reduces it to the block grid with one
-reshape + ``any`` instead of a Python loop over tiles.
+reshape + ``any`` instead of a Python loop over tiles.  With ``exact=True``
+(beyond the reference, which lists it as future work, PROGRESS.md:284-288)
+tiles whose elements are only partly visible go to the partial lists
+(``kv_*``) with their element masks as bit words (``part_row_bits`` for the
+Q-major walks, ``q_col_bits`` + ``q_partial`` for the K-major one), and the
+kernels apply those bits inside the tile: the result is attention under the
+element predicate itself instead of its block-rounded upper bound.
 
 Beyond the reference fields a mask carries a work plan (``BlockMaskPlan``,
 from ``af_blockmask_plan``): lists much longer than the mean -- BigBird's
@@ -91,6 +97,13 @@ class BlockMask:
     # when the mask was not built by block_mask_from_blocks
     plan: Optional[BlockMaskPlan] = field(default=None, repr=False,
                                           compare=False)
+    # element masks of the partial tiles (create_block_mask(exact=True)):
+    # int64 bit words (n_q_blocks, max_partial, BLOCK_M, BLOCK_N / 64) over
+    # keys, (n_kv_blocks, max_q, BLOCK_N, ceil(BLOCK_M / 64)) over queries,
+    # and int32 (n_kv_blocks, max_q) flags of the partial K-major entries
+    part_row_bits: Optional[torch.Tensor] = field(default=None, repr=False)
+    q_col_bits: Optional[torch.Tensor] = field(default=None, repr=False)
+    q_partial: Optional[torch.Tensor] = field(default=None, repr=False)
 
     def to(self, device) -> "BlockMask":
         f = {k: (v.to(device) if isinstance(v, (torch.Tensor, BlockMaskPlan))
@@ -140,6 +153,10 @@ class BlockMask:
         bm.n_kv_items = pl.kv_items.shape[0]
         bm.n_kv_splits = pl.kv_splits.shape[0]
         bm.n_kv_slots = pl.n_kv_slots
+        if self.part_row_bits is not None:
+            bm.part_row_bits = self.part_row_bits.data_ptr()
+            bm.q_col_bits = self.q_col_bits.data_ptr()
+            bm.q_partial = self.q_partial.data_ptr()
         return bm
 
 
@@ -177,18 +194,89 @@ def block_mask_from_blocks(active: torch.Tensor, BLOCK_M: int, BLOCK_N: int,
         n_active=n, n_full=n, plan=plan)
 
 
+def _pack_bits(bits: torch.Tensor) -> torch.Tensor:
+    """(..., 64 w) bool -> (..., w) int64 words, element k of a word in bit
+    k (bit 63 comes out as the int64 sign bit)."""
+    *lead, n = bits.shape
+    b = bits.reshape(*lead, n // 64, 64).to(torch.int64)
+    return (b << torch.arange(64, dtype=torch.int64)).sum(dim=-1)
+
+
+def block_mask_from_elements(elem: torch.Tensor, BLOCK_M: int, BLOCK_N: int,
+                             device="cuda") -> BlockMask:
+    """BlockMask that applies the (Q_LEN, KV_LEN) bool element mask ``elem``
+    exactly: tiles with every element visible go to the full lists, tiles
+    with some to the partial lists with their bits, tiles with none nowhere.
+    Elements past the sequence ends count as visible for the full/partial
+    test (the kernels mask them by length)."""
+    if BLOCK_N % 64:
+        raise NotImplementedError("element masks need BLOCK_N a multiple "
+                                  "of 64")
+    elem = elem.to(torch.bool).cpu()
+    Q_LEN, KV_LEN = elem.shape
+    nqb = (Q_LEN + BLOCK_M - 1) // BLOCK_M
+    nkb = (KV_LEN + BLOCK_N - 1) // BLOCK_N
+    vis = torch.zeros(nqb * BLOCK_M, nkb * BLOCK_N, dtype=torch.bool)
+    vis[:Q_LEN, :KV_LEN] = elem
+    dont_care = torch.ones_like(vis)
+    dont_care[:Q_LEN, :KV_LEN] = elem
+    tiles = vis.view(nqb, BLOCK_M, nkb, BLOCK_N).permute(0, 2, 1, 3)
+    anyv = tiles.any(dim=3).any(dim=2)
+    allv = dont_care.view(nqb, BLOCK_M, nkb, BLOCK_N).all(dim=3).all(dim=1)
+    full = anyv & allv
+    part = anyv & ~allv
+    full_num, full_idx = _csr_rows(full)
+    part_num, part_idx = _csr_rows(part)
+    q_num, q_idx = _csr_rows(anyv.t().contiguous())
+    # Q-major row bits: partial tile (qb, kb) is entry rank(kb) of row qb
+    wr = BLOCK_N // 64
+    row_bits = torch.zeros(nqb, part_idx.shape[1], BLOCK_M, wr,
+                           dtype=torch.int64)
+    qb, kb = part.nonzero(as_tuple=True)
+    if qb.numel():
+        e = (part.cumsum(dim=1) - 1)[qb, kb]
+        row_bits[qb, e] = _pack_bits(tiles[qb, kb])
+    # K-major column bits and partial flags: entry rank(qb) of column kb
+    wc = (BLOCK_M + 63) // 64
+    col_bits = torch.zeros(nkb, q_idx.shape[1], BLOCK_N, wc, dtype=torch.int64)
+    q_partial = torch.zeros(nkb, q_idx.shape[1], dtype=torch.int32)
+    if qb.numel():
+        j = (anyv.t().cumsum(dim=1) - 1)[kb, qb]
+        cols = tiles[qb, kb].transpose(1, 2)            # (n, BLOCK_N, BLOCK_M)
+        if BLOCK_M % 64:
+            cols = torch.cat([cols, torch.zeros(*cols.shape[:2], 64 * wc - BLOCK_M,
+                                                dtype=torch.bool)], dim=2)
+        col_bits[kb, j] = _pack_bits(cols)
+        q_partial[kb, j] = 1
+    plan = (make_plan(full_num + part_num, q_num, device)
+            if torch.device(device).type == "cuda" else None)
+    n_full, n_part = int(full_num.sum()), int(part_num.sum())
+    return BlockMask(
+        kv_num_blocks=part_num.to(device), kv_indices=part_idx.to(device),
+        full_kv_num=full_num.to(device), full_kv_idx=full_idx.to(device),
+        q_num_blocks=q_num.to(device), q_indices=q_idx.to(device),
+        BLOCK_M=BLOCK_M, BLOCK_N=BLOCK_N, n_q_blocks=nqb, n_kv_blocks=nkb,
+        n_active=n_full + n_part, n_full=n_full, plan=plan,
+        part_row_bits=row_bits.to(device), q_col_bits=col_bits.to(device),
+        q_partial=q_partial.to(device))
+
+
 def create_block_mask(mask_fn: Callable, Q_LEN: int, KV_LEN: int,
                       BLOCK_M: int = 64, BLOCK_N: int = 64,
-                      device="cuda") -> BlockMask:
+                      device="cuda", exact: bool = False) -> BlockMask:
     """BlockMask from an element predicate ``mask_fn(q_idx, kv_idx) -> bool``
     evaluated on (Q_LEN, KV_LEN) index grids.  A tile with any True element
-    is active (and visited whole)."""
+    is active; by default it is visited whole (the reference's rounding),
+    with ``exact=True`` partly visible tiles carry their element bits and
+    the kernels apply the predicate itself."""
     nqb = (Q_LEN + BLOCK_M - 1) // BLOCK_M
     nkb = (KV_LEN + BLOCK_N - 1) // BLOCK_N
     qi = torch.arange(Q_LEN)[:, None].expand(Q_LEN, KV_LEN)
     kj = torch.arange(KV_LEN)[None, :].expand(Q_LEN, KV_LEN)
     elem = torch.as_tensor(mask_fn(qi, kj), dtype=torch.bool)
     elem = elem.expand(Q_LEN, KV_LEN)
+    if exact:
+        return block_mask_from_elements(elem, BLOCK_M, BLOCK_N, device)
     padded = torch.zeros(nqb * BLOCK_M, nkb * BLOCK_N, dtype=torch.bool)
     padded[:Q_LEN, :KV_LEN] = elem
     active = padded.view(nqb, BLOCK_M, nkb, BLOCK_N).any(dim=3).any(dim=1)

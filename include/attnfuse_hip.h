@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define AF_ABI_VERSION 5
+#define AF_ABI_VERSION 6
 
 typedef enum af_status {
   AF_OK = 0,
@@ -98,6 +98,22 @@ typedef struct af_blockmask {
   const int32_t* kv_splits; /* (n_kv_splits, 3) */
   int32_t n_q_items, n_q_splits, n_q_slots;
   int32_t n_kv_items, n_kv_splits, n_kv_slots;
+  /* Optional element masks of the partial tiles (kv_indices entries), all
+   * three NULL or all three set.  No counterpart in the reference, which
+   * visits a partial tile whole (attnfuse/runtime/block_mask.py:139-151) and
+   * lists element masks as future work (PROGRESS.md:284-288).  Device
+   * uint64 words, a set bit = visible:
+   *   part_row_bits (n_q_blocks, kv_stride, block_m, block_n / 64): word w of
+   *     row r of query block qb's partial entry e covers keys
+   *     64 w .. 64 w + 63 of that entry's key block;
+   *   q_col_bits (n_kv_blocks, q_stride, block_n, ceil(block_m / 64)): word w
+   *     of key column c of key block kb's K-major entry e covers queries
+   *     64 w .. 64 w + 63 of that entry's query block (dK/dV);
+   *   q_partial (n_kv_blocks, q_stride) int32: 1 where K-major entry e of key
+   *     block kb is a partial tile (its q_col_bits apply). */
+  const uint64_t* part_row_bits;
+  const uint64_t* q_col_bits;
+  const int32_t* q_partial;
 } af_blockmask;
 
 /* Work plan of a block-sparse walk over lists of counts[i] entries (Q-major:

@@ -238,6 +238,28 @@ def block_grid(pred, q_len: int, kv_len: int, bm: int, bn: int) -> torch.Tensor:
     return grid
 
 
+def block_classes(pred, q_len: int, kv_len: int, bm: int, bn: int):
+    """(full, partial) bool tile grids of an element predicate, by the
+    per-tile loop of the reference's create_block_mask
+    (attnfuse/runtime/block_mask.py:129-151) over tiles clipped to the
+    sequence ends: full when every element of the tile is visible, partial
+    when some but not all are (the reference then rounds partial up to full;
+    an exact mask keeps them apart)."""
+    nqb, nkb = -(-q_len // bm), -(-kv_len // bn)
+    qi = torch.arange(q_len)[:, None].expand(q_len, kv_len)
+    kj = torch.arange(kv_len)[None, :].expand(q_len, kv_len)
+    elem = torch.as_tensor(pred(qi, kj), dtype=torch.bool).expand(q_len, kv_len)
+    full = torch.zeros(nqb, nkb, dtype=torch.bool)
+    part = torch.zeros(nqb, nkb, dtype=torch.bool)
+    for a in range(nqb):
+        for b in range(nkb):
+            tile = elem[a * bm:(a + 1) * bm, b * bn:(b + 1) * bn]
+            n = int(tile.sum())
+            full[a, b] = n == tile.numel()
+            part[a, b] = 0 < n < tile.numel()
+    return full, part
+
+
 def block_lists(grid: torch.Tensor):
     """Q-major rows and K-major columns of a tile grid as Python lists."""
     rows = [[b for b in range(grid.shape[1]) if grid[a, b]]

@@ -23,7 +23,7 @@ def _declared_functions():
 
 def test_library_loads_and_reports_abi():
     lib = N.lib()
-    assert lib.af_abi_version() == 5
+    assert lib.af_abi_version() == 6
 
 
 def test_every_declared_symbol_is_exported():
