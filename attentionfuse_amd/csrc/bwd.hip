@@ -29,19 +29,6 @@ int bwd_group_split(const af_bwd_args& a) {
   return gs;
 }
 
-// fp32 dK/dV: split the group's query heads until the grid holds about four
-// 4-wave workgroups per CU (256 CUs); causal key blocks differ in work by up
-// to N/128 times, so one workgroup per key block leaves most CUs idle at the end.
-int bwd_group_split_f32(const af_bwd_args& a) {
-  if (a.group_split > 0 && group_split_valid(a)) return a.group_split;
-  if (a.batch <= 0 || a.heads_kv <= 0 || a.heads_q <= 0 || a.seqlen_kv <= 0 || a.heads_q % a.heads_kv != 0) return 1;
-  const int G = a.heads_q / a.heads_kv;
-  const int64_t base = (int64_t)((a.seqlen_kv + 127) / 128) * a.batch * a.heads_kv;
-  int gs = 1;
-  while (G % (2 * gs) == 0 && base * 2 * gs <= 1024) gs *= 2;
-  return gs;
-}
-
 // The block mask's K-major plan is used when its columns are split and the
 // GQA query heads are not: the library then keeps the heads together (the
 // column pieces already fill the grid) unless the caller asks for a split.
@@ -50,7 +37,6 @@ static bool kv_plan_wanted(const af_bwd_args& a, const af_blockmask* bm) {
 }
 
 int bwd_group_split_for(const af_bwd_args& a, const af_blockmask* bm) {
-  if (a.key.dtype == AF_F32) return bwd_group_split_f32(a);
   if (kv_plan_wanted(a, bm) && bm->n_kv_splits > 0 && a.group_split == 0) return 1;
   return bwd_group_split(a);
 }

@@ -1,5 +1,7 @@
 // Launch sequence of the fp32 backward (bwd_f32_kernel.hpp): RoPE of q and k
-// into the workspace, the per-row prep, then the dK/dV and dQ kernels.
+// into the workspace, the per-row prep, then the dK/dV and dQ workgroups
+// (one launch when both use the same workgroup width) and the sum of the
+// group-split dK/dV partials.
 #include "attnfuse_hip.h"
 #include "bwd_f32_kernel.hpp"
 #include "launch.hpp"
@@ -14,23 +16,32 @@ static void launch_bwd_f32_d(BwdParams p, int mask, int bias, int rope, int wkv,
   if (rows_q > 0)
     hipLaunchKernelGGL((bwd_prep_f32_kernel<D>), dim3((unsigned)((rows_q + 255) / 256)), dim3(256), 0, s, p);
   const unsigned grid_kv = (unsigned)(p.n_kblocks * p.g_split * p.B * p.Hkv);
-  if (grid_kv > 0) {
+  const unsigned grid_q = (unsigned)(p.n_qblocks * p.B * p.Hq);
+  if (wkv == wq && grid_kv > 0 && grid_q > 0) {
+    // dK/dV and dQ workgroups in one launch, dK/dV first
+    BwdParams q = p;
+    q.n_dkv_wg = (int32_t)grid_kv;
     if (wkv == 2)
-      hipLaunchKernelGGL((bwd_dkv_f32_kernel<D, 2>), dim3(grid_kv), dim3(128), 0, s, p, mask, bias, rope);
+      hipLaunchKernelGGL((bwd_dkvdq_f32_kernel<D, 2>), dim3(grid_kv + grid_q), dim3(128), 0, s, q, mask, bias, rope);
     else
-      hipLaunchKernelGGL((bwd_dkv_f32_kernel<D, 4>), dim3(grid_kv), dim3(256), 0, s, p, mask, bias, rope);
-    if (p.g_split > 1) {
-      const int64_t threads = (int64_t)p.B * p.Hkv * p.Nkv * (D / 4);
-      hipLaunchKernelGGL((bwd_dkv_combine_f32_kernel<D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                         p);
+      hipLaunchKernelGGL((bwd_dkvdq_f32_kernel<D, 4>), dim3(grid_kv + grid_q), dim3(256), 0, s, q, mask, bias, rope);
+  } else {
+    if (grid_kv > 0) {
+      if (wkv == 2)
+        hipLaunchKernelGGL((bwd_dkv_f32_kernel<D, 2>), dim3(grid_kv), dim3(128), 0, s, p, mask, bias, rope);
+      else
+        hipLaunchKernelGGL((bwd_dkv_f32_kernel<D, 4>), dim3(grid_kv), dim3(256), 0, s, p, mask, bias, rope);
+    }
+    if (grid_q > 0) {
+      if (wq == 2)
+        hipLaunchKernelGGL((bwd_dq_f32_kernel<D, 2>), dim3(grid_q), dim3(128), 0, s, p, mask, bias, rope);
+      else
+        hipLaunchKernelGGL((bwd_dq_f32_kernel<D, 4>), dim3(grid_q), dim3(256), 0, s, p, mask, bias, rope);
     }
   }
-  const unsigned grid_q = (unsigned)(p.n_qblocks * p.B * p.Hq);
-  if (grid_q > 0) {
-    if (wq == 2)
-      hipLaunchKernelGGL((bwd_dq_f32_kernel<D, 2>), dim3(grid_q), dim3(128), 0, s, p, mask, bias, rope);
-    else
-      hipLaunchKernelGGL((bwd_dq_f32_kernel<D, 4>), dim3(grid_q), dim3(256), 0, s, p, mask, bias, rope);
+  if (grid_kv > 0 && p.g_split > 1) {
+    const int64_t threads = (int64_t)p.B * p.Hkv * p.Nkv * (D / 4);
+    hipLaunchKernelGGL((bwd_dkv_combine_f32_kernel<D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, p);
   }
 }
 

@@ -82,23 +82,27 @@ __device__ __forceinline__ void f32_rope_back(float& lo, float& hi, float clo, f
   hi = b;
 }
 
-template <int D, int WAVES = kBwdF32Waves>
-__global__ void __launch_bounds__(WAVES * 64) bwd_dkv_f32_kernel(const BwdParams p, int mask, int bias, int rope) {
-  constexpr int DH = D / 2, DC = D / 32, QP = D + 4;
+// LDS of either body: two (32 x (D + 4)) fp32 tiles (q~ and dO rows for
+// dK/dV, k~ and v rows for dQ).
+template <int D>
+using F32Tile = float[32][D + 4];
+
+// dK/dV body of workgroup wg; ql / gl: the two LDS tiles.
+template <int D, int WAVES>
+__device__ __forceinline__ void bwd_dkv_f32_body(const BwdParams& p, int mask, int bias, int rope, F32Tile<D>& ql,
+                                                 F32Tile<D>& gl, int wg) {
+  constexpr int DH = D / 2, DC = D / 32;
   constexpr int BLK = 32 * WAVES;
   typedef typename F32Vec<DC>::T VecC;
-  // the current query tile's q~ and dO rows, shared by the four waves
-  __shared__ __attribute__((aligned(16))) float ql[32][QP];
-  __shared__ __attribute__((aligned(16))) float gl[32][QP];
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int col = lane & 31, h = lane >> 5;
   // workgroup = (key block, group split, b, h_kv), key block slowest; split
   // gsi takes query heads [gsi G/g_split, (gsi + 1) G/g_split) of the group
   const int nbh = p.B * p.Hkv;
-  const int kb = (int)(blockIdx.x / (nbh * p.g_split));
-  const int gsi = (int)(blockIdx.x / nbh) % p.g_split;
-  const int bh = (int)(blockIdx.x % nbh);
+  const int kb = wg / (nbh * p.g_split);
+  const int gsi = (wg / nbh) % p.g_split;
+  const int bh = wg % nbh;
   const int b = bh / p.Hkv, hk = bh % p.Hkv;
   const int kw0 = kb * BLK;  // first key of the workgroup
   const int gpw = p.G / p.g_split;
@@ -312,20 +316,19 @@ __global__ void __launch_bounds__(256) bwd_dkv_combine_f32_kernel(const BwdParam
                             d) = sv;
 }
 
-template <int D, int WAVES = kBwdF32Waves>
-__global__ void __launch_bounds__(WAVES * 64) bwd_dq_f32_kernel(const BwdParams p, int mask, int bias, int rope) {
-  constexpr int DH = D / 2, DC = D / 32, KP = D + 4;
+// dQ body of workgroup wg; kl / vl: the two LDS tiles.
+template <int D, int WAVES>
+__device__ __forceinline__ void bwd_dq_f32_body(const BwdParams& p, int mask, int bias, int rope, F32Tile<D>& kl,
+                                                F32Tile<D>& vl, int wg) {
+  constexpr int DH = D / 2, DC = D / 32;
   constexpr int BLK = 32 * WAVES;
   typedef typename F32Vec<DC>::T VecC;
-  // the current key tile's k~ and v rows, shared by the four waves
-  __shared__ __attribute__((aligned(16))) float kl[32][KP];
-  __shared__ __attribute__((aligned(16))) float vl[32][KP];
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int col = lane & 31, h = lane >> 5;
   const int nbh = p.B * p.Hq;
-  int mb = (int)(blockIdx.x / nbh);
-  const int bh = (int)(blockIdx.x % nbh);
+  int mb = wg / nbh;
+  const int bh = wg % nbh;
   if (mask == MASK_CAUSAL || mask == MASK_CSW) mb = p.n_qblocks - 1 - mb;
   const int b = bh / p.Hq, hq = bh % p.Hq, hk = hq / p.G;
   const int qw0 = mb * BLK;  // first query of the workgroup
@@ -487,6 +490,32 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_dq_f32_kernel(const BwdParams 
     }
     *reinterpret_cast<VecC*>(dqr + d0) = st;
   }
+}
+
+// The dK/dV and dQ kernels, one launch each, and both in one launch: its
+// first n_dkv_wg workgroups run the dK/dV body (heaviest key blocks first
+// under a causal mask), the rest the dQ body, whose workgroups fill the
+// slots the short causal dK/dV workgroups free at the end of the first.
+template <int D, int WAVES = kBwdF32Waves>
+__global__ void __launch_bounds__(WAVES * 64) bwd_dkv_f32_kernel(const BwdParams p, int mask, int bias, int rope) {
+  __shared__ __attribute__((aligned(16))) F32Tile<D> ql, gl;
+  bwd_dkv_f32_body<D, WAVES>(p, mask, bias, rope, ql, gl, (int)blockIdx.x);
+}
+
+template <int D, int WAVES = kBwdF32Waves>
+__global__ void __launch_bounds__(WAVES * 64) bwd_dq_f32_kernel(const BwdParams p, int mask, int bias, int rope) {
+  __shared__ __attribute__((aligned(16))) F32Tile<D> kl, vl;
+  bwd_dq_f32_body<D, WAVES>(p, mask, bias, rope, kl, vl, (int)blockIdx.x);
+}
+
+template <int D, int WAVES = kBwdF32Waves>
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
+    bwd_dkvdq_f32_kernel(const BwdParams p, int mask, int bias, int rope) {
+  __shared__ __attribute__((aligned(16))) F32Tile<D> ta, tb;
+  if ((int)blockIdx.x < p.n_dkv_wg)
+    bwd_dkv_f32_body<D, WAVES>(p, mask, bias, rope, ta, tb, (int)blockIdx.x);
+  else
+    bwd_dq_f32_body<D, WAVES>(p, mask, bias, rope, ta, tb, (int)blockIdx.x - p.n_dkv_wg);
 }
 
 }  // namespace af

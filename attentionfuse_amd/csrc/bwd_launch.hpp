@@ -32,13 +32,14 @@ struct BwdWorkspace {
 // grid stays within two workgroups per CU (512), so that a causal mask's
 // long key blocks do not leave most CUs idle.  Measured at config 5 (256
 // workgroups unsplit, one per CU): backward 1153 us unsplit, 796 us split 4
-// ways, 773 us split 2 ways; at B = 2 (512 workgroups) splitting lost.
+// ways, 773 us split 2 ways; at B = 2 (512 workgroups) splitting lost.  The
+// fp32 kernels use the same rule: with dK/dV and dQ in one launch, config 5
+// in fp32 takes 8.97 ms unsplit, 6.38-6.39 ms split 2 ways, 6.44 ms 4 ways.
 // The args' group_split when it is set, else the choice described above.
 int bwd_group_split(const af_bwd_args& a);
 bool group_split_valid(const af_bwd_args& a);
-int bwd_group_split_f32(const af_bwd_args& a);
-// The split the launch uses: fp32's, 1 for a block mask whose K-major plan
-// splits columns (unless the caller sets group_split), else bwd_group_split.
+// The split the launch uses: 1 for a block mask whose K-major plan splits
+// columns (unless the caller sets group_split), else bwd_group_split.
 int bwd_group_split_for(const af_bwd_args& a, const af_blockmask* bm);
 BwdWorkspace bwd_workspace_layout(const af_bwd_args& a, const af_blockmask* bm = nullptr);
 size_t bwd_workspace_bytes(const af_bwd_args& a, const af_blockmask* bm = nullptr);
