@@ -47,6 +47,13 @@
 
 namespace af {
 
+#ifndef AF_DKV_TR_AHEAD
+#define AF_DKV_TR_AHEAD(D) ((D) == 128 ? 4 : 0)
+#endif
+#ifndef AF_DQ_TR_AHEAD
+#define AF_DQ_TR_AHEAD(D) ((D) == 128 ? 4 : 0)
+#endif
+
 struct BwdParams {
   const uint16_t* q;
   const uint16_t* k;
@@ -344,6 +351,9 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
   constexpr int BK = 32 * WAVES;
   constexpr int KS = D / 16, DB = D / 32;
   constexpr bool VLDS = D > 64;            // V block in LDS instead of registers
+  // transposed operands of the dV/dK MFMAs read this many MFMAs ahead (0:
+  // read next to each MFMA); the 128-dim body has the registers to spare
+  constexpr int kTrAhead = AF_DKV_TR_AHEAD(D);
   constexpr int TILE = DkvLds<D, WAVES>::TILE;    // one 32-row tile (elements)
   constexpr int STAGE = DkvLds<D, WAVES>::STAGE;
   constexpr int NS = DkvLds<D, WAVES>::NS;
@@ -609,17 +619,44 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
       }
       // dV^T += dO^T P,  dK~^T += Q~^T dS   (contraction over 32 queries;
       // the transposed operands come from transposing LDS reads)
+      if constexpr (kTrAhead > 0) {
+        // MFMA i = (db, j, dV or dK) with its operand read kTrAhead MFMAs
+        // earlier; the scheduling barriers keep the compiler from sinking
+        // each read back next to its MFMA, which then waited out a whole
+        // LDS round trip (16 serialised read -> wait -> MFMA triples)
+        constexpr int NOPS = DB * 4;
+        auto read_op = [&](int i) -> u32x4 {
+          const int db = i >> 2, j = (i >> 1) & 1;
+          const uint16_t* base = ((i & 1) ? Qs : Os) + 16 * j * D;
+          const u32x2 lo = lds_read_tr16(base + tr_at<D>(lane, 0, db));
+          const u32x2 hi = lds_read_tr16(base + tr_at<D>(lane, 1, db));
+          return u32x4{lo[0], lo[1], hi[0], hi[1]};
+        };
+        u32x4 op[NOPS];
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int t0 = tr_at<D>(lane, 0, db), t1 = tr_at<D>(lane, 1, db);
+        for (int i = 0; i < kTrAhead; ++i) op[i] = read_op(i);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const u32x2 olo = lds_read_tr16(Os + 16 * j * D + t0);
-          const u32x2 ohi = lds_read_tr16(Os + 16 * j * D + t1);
-          dv[db] = E::mfma32(u32x4{olo[0], olo[1], ohi[0], ohi[1]}, pp[j], dv[db]);
-          const u32x2 qlo = lds_read_tr16(Qs + 16 * j * D + t0);
-          const u32x2 qhi = lds_read_tr16(Qs + 16 * j * D + t1);
-          dk[db] = E::mfma32(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]}, pd[j], dk[db]);
+        for (int i = 0; i < NOPS; ++i) {
+          const int db = i >> 2, j = (i >> 1) & 1;
+          if (i & 1) dk[db] = E::mfma32(op[i], pd[j], dk[db]);
+          else dv[db] = E::mfma32(op[i], pp[j], dv[db]);
+          if (i + kTrAhead < NOPS) op[i + kTrAhead] = read_op(i + kTrAhead);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const int t0 = tr_at<D>(lane, 0, db), t1 = tr_at<D>(lane, 1, db);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const u32x2 olo = lds_read_tr16(Os + 16 * j * D + t0);
+            const u32x2 ohi = lds_read_tr16(Os + 16 * j * D + t1);
+            dv[db] = E::mfma32(u32x4{olo[0], olo[1], ohi[0], ohi[1]}, pp[j], dv[db]);
+            const u32x2 qlo = lds_read_tr16(Qs + 16 * j * D + t0);
+            const u32x2 qhi = lds_read_tr16(Qs + 16 * j * D + t1);
+            dk[db] = E::mfma32(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]}, pd[j], dk[db]);
+          }
         }
       }
     }
@@ -675,6 +712,9 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
   constexpr int TILE = DqLds<D>::TILE;
   constexpr int STAGE = DqLds<D>::STAGE;
   constexpr int NS = DqLds<D>::NS;
+  // transposed K~ operands of the dQ MFMAs read this many MFMAs ahead (0:
+  // next to each MFMA)
+  constexpr int kTrAhead = AF_DQ_TR_AHEAD(D);
 
   // no queries: nothing to write (the launch still has one workgroup)
   if (p.n_qblocks <= 0) return;
@@ -852,15 +892,37 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
 #pragma unroll
         for (int i = 0; i < 4; ++i) pd[j][i] = E::pack(dsv[2 * i], dsv[2 * i + 1]);
       }
-      // dQ~^T += K~^T dS^T (contraction over 32 keys, K~^T by transposing reads)
+      // dQ~^T += K~^T dS^T (contraction over 32 keys, K~^T by transposing
+      // reads), each MFMA's operand read kTrAhead MFMAs earlier as in the
+      // dK/dV body
+      if constexpr (kTrAhead > 0) {
+        constexpr int NOPS = DB * 2;
+        auto read_op = [&](int i) -> u32x4 {
+          const int db = i >> 1, j = i & 1;
+          const u32x2 lo = lds_read_tr16(Ks + 16 * j * D + tr_at<D>(lane, 0, db));
+          const u32x2 hi = lds_read_tr16(Ks + 16 * j * D + tr_at<D>(lane, 1, db));
+          return u32x4{lo[0], lo[1], hi[0], hi[1]};
+        };
+        u32x4 op[NOPS];
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int t0 = tr_at<D>(lane, 0, db), t1 = tr_at<D>(lane, 1, db);
+        for (int i = 0; i < kTrAhead; ++i) op[i] = read_op(i);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const u32x2 klo = lds_read_tr16(Ks + 16 * j * D + t0);
-          const u32x2 khi = lds_read_tr16(Ks + 16 * j * D + t1);
-          dq[db] = E::mfma32(u32x4{klo[0], klo[1], khi[0], khi[1]}, pd[j], dq[db]);
+        for (int i = 0; i < NOPS; ++i) {
+          dq[i >> 1] = E::mfma32(op[i], pd[i & 1], dq[i >> 1]);
+          if (i + kTrAhead < NOPS) op[i + kTrAhead] = read_op(i + kTrAhead);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const int t0 = tr_at<D>(lane, 0, db), t1 = tr_at<D>(lane, 1, db);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const u32x2 klo = lds_read_tr16(Ks + 16 * j * D + t0);
+            const u32x2 khi = lds_read_tr16(Ks + 16 * j * D + t1);
+            dq[db] = E::mfma32(u32x4{klo[0], klo[1], khi[0], khi[1]}, pd[j], dq[db]);
+          }
         }
       }
     }

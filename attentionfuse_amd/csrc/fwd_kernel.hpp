@@ -281,7 +281,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // that the MFMAs, issued later, find them landed instead of each waiting
   // out one LDS round trip.
   constexpr bool kBatchK = D <= 64;
-  constexpr bool kBatchV = D <= 64;
+  constexpr bool kBatchV = D <= 128;
   // The first key block's operands are read up front; the second block's
   // are read as the first block's MFMAs issue.
   auto read_k = [&](int par, u32x4 (&kop)[KS]) {
@@ -545,7 +545,10 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // round trip of its own transposing reads).  The scheduling barriers keep
   // the compiler from sinking each read back next to its MFMA.
   constexpr int kVOps = DB * (BN / 16);
-  constexpr int kVAhead = kVOps < 4 ? kVOps : 4;
+#ifndef AF_FWD_V_AHEAD
+#define AF_FWD_V_AHEAD(D) ((D) <= 64 ? 4 : 2)
+#endif
+  constexpr int kVAhead = kVOps < AF_FWD_V_AHEAD(D) ? kVOps : AF_FWD_V_AHEAD(D);
   auto read_vop = [&](int par, int i) -> u32x4 {
     const int kk = i / DB, db = i % DB;
     const uint16_t* vt = lds + (2 + par) * TILE + 16 * kk * D;
