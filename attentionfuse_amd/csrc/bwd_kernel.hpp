@@ -53,6 +53,12 @@ namespace af {
 #ifndef AF_DQ_TR_AHEAD
 #define AF_DQ_TR_AHEAD(D) ((D) == 128 ? 4 : 0)
 #endif
+#ifndef AF_DKV_S_AHEAD
+#define AF_DKV_S_AHEAD(D) ((D) == 128 ? 2 : 0)
+#endif
+#ifndef AF_DQ_S_AHEAD
+#define AF_DQ_S_AHEAD(D) ((D) == 128 ? 2 : 0)
+#endif
 
 struct BwdParams {
   const uint16_t* q;
@@ -354,6 +360,8 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
   // transposed operands of the dV/dK MFMAs read this many MFMAs ahead (0:
   // read next to each MFMA); the 128-dim body has the registers to spare
   constexpr int kTrAhead = AF_DKV_TR_AHEAD(D);
+  // k-steps of the S and dP MFMAs whose operands are read ahead
+  constexpr int kSAhead = AF_DKV_S_AHEAD(D);
   constexpr int TILE = DkvLds<D, WAVES>::TILE;    // one 32-row tile (elements)
   constexpr int STAGE = DkvLds<D, WAVES>::STAGE;
   constexpr int NS = DkvLds<D, WAVES>::NS;
@@ -532,14 +540,37 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
     if (active) {
       // S and dP (queries x keys), query rows permuted.
       f32x16 s = f32x16{}, dp = f32x16{};
+      if constexpr (kSAhead > 0) {
+        // the q~, dO (and V) operands of k-step ks read kSAhead k-steps
+        // earlier
+        u32x4 qop[KS], oop[KS], vop[KS];
+        auto read_qo = [&](int ks) {
+          const int off = lds_at<D>(qr_row, 16 * ks + 8 * h);
+          qop[ks] = ld16(Qs + off);
+          oop[ks] = ld16(Os + off);
+          if constexpr (VLDS) vop[ks] = ld16(vblk + 32 * w * D + off);
+          else vop[ks] = vf[ks];
+        };
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int off = lds_at<D>(qr_row, 16 * ks + 8 * h);
-        s = E::mfma32(ld16(Qs + off), kf[ks], s);
-        u32x4 vb;
-        if constexpr (VLDS) vb = ld16(vblk + 32 * w * D + off);
-        else vb = vf[ks];
-        dp = E::mfma32(ld16(Os + off), vb, dp);
+        for (int ks = 0; ks < kSAhead; ++ks) read_qo(ks);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          s = E::mfma32(qop[ks], kf[ks], s);
+          dp = E::mfma32(oop[ks], vop[ks], dp);
+          if (ks + kSAhead < KS) read_qo(ks + kSAhead);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int off = lds_at<D>(qr_row, 16 * ks + 8 * h);
+          s = E::mfma32(ld16(Qs + off), kf[ks], s);
+          u32x4 vb;
+          if constexpr (VLDS) vb = ld16(vblk + 32 * w * D + off);
+          else vb = vf[ks];
+          dp = E::mfma32(ld16(Os + off), vb, dp);
+        }
       }
       float slope2 = 0.f;
       if constexpr (BIAS == BIAS_ALIBI) slope2 = p.slopes[hq] * kLog2e;
@@ -715,6 +746,8 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
   // transposed K~ operands of the dQ MFMAs read this many MFMAs ahead (0:
   // next to each MFMA)
   constexpr int kTrAhead = AF_DQ_TR_AHEAD(D);
+  // k-steps of the score MFMAs whose K~ / V operands are read ahead
+  constexpr int kSAhead = AF_DQ_S_AHEAD(D);
 
   // no queries: nothing to write (the launch still has one workgroup)
   if (p.n_qblocks <= 0) return;
@@ -827,11 +860,31 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
     if constexpr (MASK == MASK_CSW) active = active && n0 + 31 > q0w - p.window && n0 <= q0w + 31;
     if (active) {
       f32x16 s = f32x16{}, dp = f32x16{};
+      if constexpr (kSAhead > 0) {
+        // the K~ and V operands of k-step ks read kSAhead k-steps earlier
+        u32x4 kop[KS], vop[KS];
+        auto read_kv = [&](int ks) {
+          const int off = lds_at<D>(kr_row, 16 * ks + 8 * h);
+          kop[ks] = ld16(Ks + off);
+          vop[ks] = ld16(Vs + off);
+        };
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int off = lds_at<D>(kr_row, 16 * ks + 8 * h);
-        s = E::mfma32(ld16(Ks + off), qf[ks], s);
-        dp = E::mfma32(ld16(Vs + off), of[ks], dp);
+        for (int ks = 0; ks < kSAhead; ++ks) read_kv(ks);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          s = E::mfma32(kop[ks], qf[ks], s);
+          dp = E::mfma32(vop[ks], of[ks], dp);
+          if (ks + kSAhead < KS) read_kv(ks + kSAhead);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int off = lds_at<D>(kr_row, 16 * ks + 8 * h);
+          s = E::mfma32(ld16(Ks + off), qf[ks], s);
+          dp = E::mfma32(ld16(Vs + off), of[ks], dp);
+        }
       }
       bool need_mask = q0w + 32 > p.Nq || n0 + 32 > p.Nkv;
       if constexpr (MASK == MASK_CAUSAL) need_mask = need_mask || n0 + 31 > q0w;
