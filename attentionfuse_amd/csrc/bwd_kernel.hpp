@@ -107,6 +107,11 @@ struct BwdParams {
   // (unscaled, rotated space) to dkp / dvp, (g_split, B, Hkv, Nkv, D), and
   // bwd_dkv_combine_kernel adds them up.
   int32_t g_split;
+  // Only key blocks [0, n_split_kb) are split (their workgroups come first);
+  // the last, lightest ones of a causal mask run all G heads in one
+  // workgroup and store dK/dV directly.  split_keys = the key rows of the
+  // split blocks (min(n_split_kb * BLOCK_N, N_kv)), the rows the combine sums.
+  int32_t n_split_kb, split_keys;
   float* dkp;
   float* dvp;
   // Block-sparse work plans (nullable): grid row i of the dQ kernel is item
@@ -263,12 +268,14 @@ __global__ void __launch_bounds__(256) bwd_dkv_combine_kernel(const BwdParams p)
   constexpr int TPR = D / 16;
   constexpr int RPB = 256 / TPR;
   const int tid = threadIdx.x;
-  const int64_t r = (int64_t)blockIdx.x * RPB + tid / TPR;
+  // rows of the split key blocks only: (b, hk, n < split_keys)
+  const int64_t rs = (int64_t)blockIdx.x * RPB + tid / TPR;
+  if (rs >= (int64_t)p.B * p.Hkv * p.split_keys) return;
   const int64_t rows = (int64_t)p.B * p.Hkv * p.Nkv;
-  if (r >= rows) return;
   const int j = tid % TPR;
-  const int n = (int)(r % p.Nkv);
-  const int64_t bh = r / p.Nkv;
+  const int n = (int)(rs % p.split_keys);
+  const int64_t bh = rs / p.split_keys;
+  const int64_t r = bh * p.Nkv + n;
   const int hk = (int)(bh % p.Hkv), b = (int)(bh / p.Hkv);
   const int dl = 8 * j, dh = dl + D / 2;
   float vlo[8], vhi[8], klo[8], khi[8];
@@ -376,8 +383,17 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
   // most query tiles, so they are dispatched first.  Then the head-group
   // split, then (batch, key/value head).
   const int BHK = p.B * p.Hkv;
-  const int kbi = wg / (BHK * p.g_split);
-  const int rem = wg - kbi * (BHK * p.g_split);
+  // split key blocks first (g_split workgroups each), then unsplit ones
+  const int heavy_wg = p.n_split_kb * BHK * p.g_split;
+  int kbi, rem, gsplit = p.g_split;
+  if (wg < heavy_wg) {
+    kbi = wg / (BHK * p.g_split);
+    rem = wg - kbi * (BHK * p.g_split);
+  } else {
+    kbi = p.n_split_kb + (wg - heavy_wg) / BHK;
+    rem = (wg - heavy_wg) % BHK;
+    gsplit = 1;
+  }
   // block-sparse plan item: a piece [e0, e0 + ne) of column kb's list
   int kb = kbi, bs_e0 = 0, bs_ne = -1, bs_slot = -1;
   if constexpr (kIsBs<MASK>) {
@@ -392,7 +408,7 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
   const int split = rem / BHK;
   const int bhk = rem - split * BHK;
   const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
-  const int gper = p.G / p.g_split;       // query heads of this workgroup
+  const int gper = p.G / gsplit;          // query heads of this workgroup
   const int hq0 = hk * p.G + split * gper;
   const int n0 = kb * BK;
   const int n0w = n0 + 32 * w;
@@ -709,7 +725,7 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
     }
     return;
   }
-  if (p.g_split > 1) {
+  if (gsplit > 1) {
     if (key < p.Nkv) {
       const int64_t row = (((int64_t)split * p.B + b) * p.Hkv + hk) * p.Nkv + key;
       store_partial_row<D>(dv, p.dvp + row * D, h);

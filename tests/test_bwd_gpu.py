@@ -192,6 +192,22 @@ def test_backward_group_split_override(split):
         bwd._BWD_TILE.update(saved)
 
 
+@pytest.mark.parametrize("split,N,D", [(2, 1024, 128), (4, 1152, 64), (2, 1000, 64)])
+def test_backward_split_heavy_blocks_only(split, N, D):
+    """Under a causal mask only the heavy key blocks are split over the
+    head group; the last n_kblocks / (2 g_split) run whole groups and store
+    dK/dV directly (8, 9 and 8 key blocks: 2, 1 and 2 of them unsplit)."""
+    from attentionfuse_amd.runtime import backward as bwd
+    print(f"[bwd] heavy-only split={split} N={N} D={D}", flush=True)
+    saved = dict(bwd._BWD_TILE)
+    try:
+        bwd._BWD_TILE.update({"auto": False, "group_split": split})
+        check(run("rope_causal", 1, 8, 2, N, D, torch.bfloat16, base=500000.0), torch.bfloat16)
+    finally:
+        bwd._BWD_TILE.clear()
+        bwd._BWD_TILE.update(saved)
+
+
 @pytest.mark.parametrize("shape", [(2, 4, 1, 384, 64), (1, 8, 2, 640, 128), (1, 4, 4, 200, 64),
                                    (2, 6, 2, 1000, 128)])
 def test_causal_block_counts(shape):
