@@ -21,7 +21,8 @@
 //    the forward rounds them in registers.  Every query tile is read by all
 //    key blocks (and every key tile by all query blocks), so rotating once
 //    replaces one rotation (and one cos/sin read) per visit.
-//  * bwd_dkv_kernel: a workgroup owns 32*WAVES keys of one (batch, kv head);
+//  * dK/dV body (bwd_dkv_body): a workgroup owns 32*WAVES keys of one
+//    (batch, kv head);
 //    each wave owns 32 keys, k~ in registers (and v too for D <= 64; for
 //    D = 128 the workgroup's V block sits in LDS so that the dK/dV
 //    accumulators, k~ and the score tiles fit two waves per SIMD).  It walks
@@ -29,16 +30,25 @@
 //    come out group-summed with no atomics.  Scores are S (queries x keys)
 //    with the query rows permuted (kperm), so P and dS feed the dV^T and dK^T
 //    MFMAs straight from registers.
-//  * bwd_dq_kernel: a workgroup owns 32*WAVES query rows of one (batch,
-//    head); q~ and dO stay in registers; 32-key tiles of k~ and v stream
-//    through LDS.  Scores are S^T (keys x queries) so dS^T is the B operand of
-//    the dQ^T MFMA.
+//  * dQ body (bwd_dq_body): a workgroup owns 32*WAVES query rows of one
+//    (batch, head); q~ and dO stay in registers; 32-key tiles of k~ and v
+//    stream through LDS.  Scores are S^T (keys x queries) so dS^T is the B
+//    operand of the dQ^T MFMA.
+//  * bwd_dkvdq_kernel runs both bodies in one launch, dK/dV workgroups
+//    first (bwd_dkv_kernel / bwd_dq_kernel run them alone where the two
+//    bodies want different widths or registers).  The heavy key blocks of a
+//    causal mask split their GQA group over g_split workgroups that write
+//    fp32 partials, summed by bwd_dkv_combine_kernel.
+//  * In the 128-dim bodies every MFMA operand read from LDS is issued a few
+//    MFMAs (or k-steps) ahead of its MFMA (AF_*_AHEAD), so the MFMAs do not
+//    each wait out an LDS round trip.
 //  * LDS tiles are row-major with no padding and an XOR swizzle of their
 //    16-byte chunks (lds_swz): the row reads of the score MFMAs and the
 //    transposing reads (ds_read_b64_tr_b16) of the gradient MFMAs both hit
 //    64 distinct banks, so no transposed copy of any tile is stored.
-//  * Tiles are double-buffered: buffer loads (rows past the end load as
-//    zeros) of tile t+1 are in flight while tile t is on the MFMA pipes.
+//  * Tiles are staged in a ring of two or three LDS slots: buffer loads
+//    (rows past the end load as zeros) of the next tiles are in flight while
+//    tile t is on the MFMA pipes.
 #pragma once
 
 #include "af_common.hpp"
