@@ -38,6 +38,10 @@ struct FwdF32Params {
   int32_t mask, bias, norm, rope;
 };
 
+#ifndef AF_F32_TWO_K
+#define AF_F32_TWO_K(D) ((D) >= 128)
+#endif
+
 constexpr int kF32Waves = 4;          // waves (32 query rows each) per workgroup
 constexpr int kF32BlockM = 32 * kF32Waves;
 
@@ -175,16 +179,25 @@ __global__ void __launch_bounds__(kF32Waves * 64) fwd_f32_kernel(const FwdF32Par
   float m_run = -1e30f, lsum = 0.f;
 
   // K rows are clamped to the last key: loads stay in bounds and every
-  // score of a key >= N_kv is masked below.
-  f32x4 kv[DH / 4];
-  auto load_k = [&](int n0) {
+  // score of a key >= N_kv is masked below.  With two K buffers (head dims
+  // whose kernel runs one wave per SIMD anyway) tile t + 2's rows are
+  // loaded while tiles t + 1 and t are computed: one tile of compute did not
+  // cover the load latency, the score MFMAs of each tile waited for their K
+  // rows.  One buffer: tile t + 1's rows load while tile t computes.
+  constexpr bool kTwoK = AF_F32_TWO_K(D);
+  constexpr int kKAhead = kTwoK ? 2 : 1;
+  f32x4 kva[DH / 4], kvb[kTwoK ? DH / 4 : 1];
+  auto load_k = [&](f32x4 (&kv)[DH / 4], int n0) {
     const float* kr = kg + (int64_t)min(n0 + col, p.Nkv - 1) * p.ks[2] + h * DH;
 #pragma unroll
     for (int i = 0; i < DH / 4; ++i) kv[i] = *reinterpret_cast<const f32x4*>(kr + 4 * i);
   };
-  if (ntiles > 0) load_k(tile_n0(0));
+  if (ntiles > 0) load_k(kva, tile_n0(0));
+  if constexpr (kTwoK) {
+    if (ntiles > 1) load_k(kvb, tile_n0(1));
+  }
 
-  for (int t = 0; t < ntiles; ++t) {
+  auto tile = [&](int t, f32x4 (&kv)[DH / 4]) __attribute__((always_inline)) {
     const int n0 = tile_n0(t);
     VecC vv[16];
 #pragma unroll
@@ -201,7 +214,7 @@ __global__ void __launch_bounds__(kF32Waves * 64) fwd_f32_kernel(const FwdF32Par
 #pragma unroll
       for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[j][e], qv[e], s, 0, 0, 0);
     }
-    if (t + 1 < ntiles) load_k(tile_n0(t + 1));  // next tile (rows clamped, so in bounds)
+    if (t + kKAhead < ntiles) load_k(kv, tile_n0(t + kKAhead));  // rows clamped, so in bounds
 
     // element mask of a partial block-sparse tile: bits of this lane's
     // query row over the tile's 32 keys (partial entries follow the full
@@ -260,6 +273,14 @@ __global__ void __launch_bounds__(kF32Waves * 64) fwd_f32_kernel(const FwdF32Par
         else a = vv[i][c];
         o[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, x[i], o[c], 0, 0, 0);
       }
+  };
+  if constexpr (kTwoK) {
+    for (int t = 0; t < ntiles; t += 2) {
+      tile(t, kva);
+      if (t + 1 < ntiles) tile(t + 1, kvb);
+    }
+  } else {
+    for (int t = 0; t < ntiles; ++t) tile(t, kva);
   }
 
   // ---- epilogue: this lane's half of the keys plus its partner's ------------
