@@ -195,9 +195,18 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   if constexpr (kIsBs<MASK>)
     bst.init(bs_full_row, bs_nfull, bs_part_row, bs_e0, bs_sub, p.bs_block_n, BN, ntiles, lane,
              MASK == MASK_BSE ? 1 : 0);
+  // Causal-type ALiBi walks the key tiles from the diagonal down: its bias
+  // -slope (i - j) then only falls from tile to tile, so the running max set
+  // by the first (diagonal) tile holds and the later tiles take the lazy
+  // softmax step.  Walked upwards the max rose by slope * 64 per tile and
+  // every step had to compute it.
+  constexpr bool kDescend =
+      BIAS == BIAS_ALIBI && NORM == NORM_SOFTMAX && (MASK == MASK_CAUSAL || MASK == MASK_CSW);
   auto tile_n0 = [&](int t) -> int {
     if constexpr (kIsBs<MASK>) {
       return bst(t);
+    } else if constexpr (kDescend) {
+      return n_lo + (ntiles - 1 - t) * BN;
     } else {
       return n_lo + t * BN;
     }
@@ -672,10 +681,11 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     wait_lds_dma();
     __syncthreads();
   };
-  // ALiBi raises a row's max on nearly every tile while the keys approach
-  // the query (by slope * 64 per tile), so ALiBi steps stay exact: the
-  // rescale in registers is far cheaper than recomputing the tile.
-  constexpr bool kLazy = NORM == NORM_SOFTMAX && BIAS != BIAS_ALIBI;
+  // Walked towards the query, ALiBi raises a row's max on nearly every tile
+  // (by slope * 64), so two-sided ALiBi steps stay exact: the rescale in
+  // registers is far cheaper than recomputing the tile.  Causal-type ALiBi
+  // walks away from the query (kDescend) and is lazy like the rest.
+  constexpr bool kLazy = NORM == NORM_SOFTMAX && (BIAS != BIAS_ALIBI || kDescend);
   if constexpr (kLazy) {
     if (ntiles > 0) {
       issue(0, 0);
