@@ -41,6 +41,9 @@ def variant(name, H, window=32, scale=None):
         return lambda Q, K, V: af.softmax(af.alibi(af.scaled_dot_product(Q, K), H)) @ V
     if name == "causal_alibi":
         return lambda Q, K, V: af.softmax(af.causal(af.alibi(af.scaled_dot_product(Q, K), H))) @ V
+    if name == "sw_causal_alibi":
+        return lambda Q, K, V: af.softmax(af.causal(af.sliding_window(
+            af.alibi(af.scaled_dot_product(Q, K), H), window))) @ V
     if name == "additive":
         return lambda Q, K, V: af.softmax(af.additive_bias(af.scaled_dot_product(Q, K))) @ V
     if name == "relu_causal":
@@ -73,10 +76,10 @@ def oracle_kwargs(name, H, Q, window=32, scale=None, bias=None, rope=None):
     return kw
 
 
-def run_case(name, B, Hq, Hkv, N, D, dtype, Nkv=None, scale=None, seed=0):
+def run_case(name, B, Hq, Hkv, N, D, dtype, Nkv=None, scale=None, seed=0, window=32):
     Nkv = N if Nkv is None else Nkv
     Q, K, V = make(B, Hq, Hkv, N, Nkv, D, dtype, seed)
-    fn = af.attention(variant(name, Hq, scale=scale))
+    fn = af.attention(variant(name, Hq, window=window, scale=scale))
     extra, rope, bias = {}, None, None
     if name.startswith("rope"):
         cos, sin = build_rope_cache(max(N, Nkv), D, device="cuda", dtype=dtype)
@@ -89,15 +92,26 @@ def run_case(name, B, Hq, Hkv, N, D, dtype, Nkv=None, scale=None, seed=0):
     out = fn(Q, K, V, **extra)
     torch.cuda.synchronize()
     want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(),
-                             **oracle_kwargs(name, Hq, Q, scale=scale,
+                             **oracle_kwargs(name, Hq, Q, window=window, scale=scale,
                                              bias=None if bias is None else bias.cpu(),
                                              rope=rope))
     err = (out.float().cpu() - want).abs().max().item()
     return err
 
 
-VARIANTS = ["dense", "causal", "sw", "sw_causal", "alibi", "causal_alibi",
+VARIANTS = ["dense", "causal", "sw", "sw_causal", "alibi", "causal_alibi", "sw_causal_alibi",
             "additive", "relu", "relu_causal", "rope_causal", "rope_causal_alibi"]
+
+
+@pytest.mark.parametrize("name,N,window", [("causal_alibi", 1000, 32), ("rope_causal_alibi", 1536, 32),
+                                           ("sw_causal_alibi", 1000, 300)])
+def test_causal_alibi_descending_walk(name, N, window):
+    """Causal-type ALiBi walks its key tiles from the diagonal down with the
+    lazy softmax step: long rows (16-24 tiles), a ragged length and a
+    causal window, fp16, against the oracle."""
+    print(f"[fwd] {name} N={N} window={window}", flush=True)
+    err = run_case(name, 1, 8, 8, N, 64, torch.float16, seed=N, window=window)
+    assert err <= TOL[torch.float16], f"{name}: max|err|={err:.3e}"
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
