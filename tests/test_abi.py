@@ -181,3 +181,44 @@ def test_decode_split_and_workspace_arithmetic():
     assert lib.af_decode(a, None, 0, None) == N.AF_ERR_WORKSPACE
     a.key = N.SpecKeyC(1, 128, 1, 0, 0, 0)
     assert lib.af_decode(a, None, 0, None) == N.AF_ERR_UNSUPPORTED
+
+
+def test_element_mask_arguments_are_checked_before_any_launch():
+    """af_fwd_blocksparse / af_bwd refuse element masks given only in part
+    and element masks at head dim 256, from the arguments alone."""
+    lib = N.lib()
+    D, Nn = 64, 128
+    a = N.FwdArgsC()
+    a.key = N.SpecKeyC(0, D, 3, 0, 0, 0)
+    a.batch, a.heads_q, a.heads_kv, a.seqlen_q, a.seqlen_kv = 1, 2, 2, Nn, Nn
+    a.q = a.k = a.v = a.o = 256
+    for s in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
+        s[:] = (2 * Nn * D, Nn * D, D, 1)
+    a.scale = 0.125
+    bm = N.BlockMaskC()
+    bm.full_kv_num = bm.full_kv_idx = bm.kv_num_blocks = bm.kv_indices = 256
+    bm.q_num_blocks = bm.q_indices = 256
+    bm.full_kv_stride = bm.kv_stride = bm.q_stride = 2
+    bm.block_m = bm.block_n = 64
+    bm.n_q_blocks = bm.n_kv_blocks = 2
+    bm.part_row_bits = 256                         # the other two missing
+    assert lib.af_fwd_blocksparse(a, bm, None, 0, None) == N.AF_ERR_BAD_ARG
+    assert "all NULL or all set" in N.last_error()
+    bm.q_col_bits = bm.q_partial = 256
+    a.key = N.SpecKeyC(0, 256, 3, 0, 0, 0)
+    for s in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
+        s[:] = (2 * Nn * 256, Nn * 256, 256, 1)
+    assert lib.af_fwd_blocksparse(a, bm, None, 0, None) == N.AF_ERR_UNSUPPORTED
+    assert "128" in N.last_error()
+    b = N.BwdArgsC()
+    b.key = N.SpecKeyC(0, D, 3, 0, 0, 0)
+    b.q = b.k = b.v = b.o = b.dout = b.dq = b.dk = b.dv = b.lse = 256
+    for s in (b.q_stride, b.k_stride, b.v_stride, b.o_stride, b.do_stride, b.dq_stride, b.dk_stride, b.dv_stride):
+        s[:] = (2 * Nn * D, Nn * D, D, 1)
+    b.lse_stride[:] = (2 * Nn, Nn, 1)
+    b.batch, b.heads_q, b.heads_kv, b.seqlen_q, b.seqlen_kv = 1, 2, 2, Nn, Nn
+    b.scale = 0.125
+    bm.q_partial = None
+    ws = int(lib.af_bwd_blocksparse_workspace_bytes(b, bm))
+    assert lib.af_bwd(b, bm, 256, ws, None) == N.AF_ERR_BAD_ARG
+    assert "all NULL or all set" in N.last_error()
