@@ -157,3 +157,28 @@ def test_elem_causal_matches_dense_causal_kernel():
     want = fn(Q, K, V)
     torch.cuda.synchronize()
     assert (got.float() - want.float()).abs().max().item() <= 1e-3
+
+
+@pytest.mark.parametrize("name", ["causal", "mixed"])
+def test_elem_walks_longer_than_64_tiles(name):
+    """Lists of 72 entries (no plan split): tiles from 64 on are looked up in
+    the lists rather than the per-lane table, partial-tile flags included
+    (causal: the Q-major diagonal entry comes last; mixed: every tile is
+    partial, so the K-major flags are read for entries past 64)."""
+    print(f"[bs-elem] long walks {name}", flush=True)
+    n, D, dtype = 72, 64, torch.float16
+    N = 64 * n
+    pred = PREDS["causal"] if name == "causal" else (lambda q, k: (q + k) % 3 != 0)
+    g = torch.Generator(device="cuda").manual_seed(23)
+    Q, K, V, dO = (rand((1, 1, N, D), dtype, g) for _ in range(4))
+    bm = af.create_block_mask(pred, N, N, 64, 64, device="cuda", exact=True)
+    assert int(bm.full_kv_num.max() + bm.kv_num_blocks.max()) >= 64
+    assert bm.plan.q_splits.shape[0] == 0 and bm.plan.kv_splits.shape[0] == 0
+    lse = torch.empty(Q.shape[:3], device="cuda", dtype=torch.float32)
+    out = run_block_sparse(Q, K, V, bm, D ** -0.5, save_lse=lse)
+    dq, dk, dv = run_block_sparse_backward(Q, K, V, out, lse, dO, bm, D ** -0.5)
+    torch.cuda.synchronize()
+    o_ref, rq, rk, rv = O.attention_grads(Q.cpu(), K.cpu(), V.cpu(), dO.cpu(), dtype=torch.float32,
+                                          elem_mask=elem_mask(pred, N, N))
+    assert (out.float().cpu() - o_ref).abs().max().item() <= TOL[dtype]
+    grads_ok((dq, dk, dv), (rq, rk, rv), dtype)
