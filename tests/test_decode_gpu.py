@@ -112,3 +112,19 @@ def test_concurrent_decodes_on_two_streams():
         want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu())
         err = (outs[name].float().cpu() - want).abs().max().item()
         assert err <= TOL[dt], (name, err)
+
+
+@pytest.mark.parametrize("alibi", [False, True], ids=["plain", "alibi"])
+def test_decode_long_cache(alibi):
+    """A 262144-key cache (1 GiB of K/V, 64 splits of 4096 keys): every key
+    counted once, against the oracle; with ALiBi the query sits at N - 1."""
+    B, Hq, Hkv, N, D = 1, 32, 8, 262144, 128
+    print(f"[decode] long cache N={N} alibi={alibi}", flush=True)
+    Q, K, V = make(B, Hq, Hkv, N, D, torch.bfloat16, seed=9)
+    out = (alibi_fn(Hq) if alibi else dense)(Q, K, V)
+    torch.cuda.synchronize()
+    kw = {}
+    if alibi:
+        kw = {"alibi_slopes": _alibi_slopes(Hq, "cpu", "torch.bfloat16").float(), "query_offset": N - 1}
+    want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(), **kw)
+    assert (out.float().cpu() - want).abs().max().item() <= TOL[torch.bfloat16]
