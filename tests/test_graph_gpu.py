@@ -97,3 +97,69 @@ def test_decode_graph_replays_match_eager():
     torch.cuda.synchronize()
     ref2 = O.naive_attention(Q.cpu(), K.cpu(), V.cpu())
     assert (out.float().cpu() - ref2).abs().max().item() <= 1.6e-2
+
+
+@pytest.mark.parametrize("kind", ["gqa_rope", "block_sparse"])
+def test_training_step_graph_replays_match_eager(kind):
+    """A whole training step -- forward (saving L) and backward, RoPE + GQA
+    with the head-group split, or a block-sparse walk with a split plan --
+    captured once: every replay equals the eager step bit for bit, and the
+    gradients match the oracle."""
+    from attentionfuse_amd.runtime.backward import run_backward
+    from attentionfuse_amd.runtime.block_mask import (block_mask_from_blocks, run_block_sparse,
+                                                      run_block_sparse_backward)
+    print(f"[graph train] {kind}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(6)
+    dtype = torch.bfloat16
+    if kind == "gqa_rope":
+        B, Hq, Hkv, N, D = 1, 8, 2, 1024, 128
+    else:
+        B, Hq, Hkv, N, D = 1, 2, 2, 1024, 64
+    Q = torch.randn(B, Hq, N, D, generator=g, device="cuda", dtype=dtype)
+    K, V = (torch.randn(B, Hkv, N, D, generator=g, device="cuda", dtype=dtype) for _ in range(2))
+    dO = torch.randn(B, Hq, N, D, generator=g, device="cuda", dtype=dtype)
+    L = torch.empty(B, Hq, N, dtype=torch.float32, device="cuda")
+    res = {}
+    if kind == "gqa_rope":
+        cos, sin = build_rope_cache(N, D, base=500000.0, device="cuda", dtype=dtype)
+        graph_ir = af.attention(lambda Q, K, V: af.softmax(af.causal(af.rope(Q, K))) @ V)(
+            Q, K, V, return_graph=True)
+        fwd, out = prepare_attention(graph_ir, Q, K, V, cos=cos, sin=sin, save_lse=L)
+
+        def step():
+            fwd()
+            res["g"] = run_backward(graph_ir, Q, K, V, out, L, dO, D ** -0.5, cos=cos, sin=sin)
+        kw = {"causal": True, "rope": (cos[0, 0].cpu(), sin[0, 0].cpu())}
+    else:
+        n = N // 64
+        grid = torch.zeros(n, n, dtype=torch.bool)
+        grid[0, :] = grid[:, 0] = True
+        for i in range(n):
+            grid[i, max(i - 1, 0): i + 2] = True
+        bm = block_mask_from_blocks(grid, 64, 64, device="cuda")
+        bm.plan_work(2)
+        out = torch.empty_like(Q)
+
+        def step():
+            run_block_sparse(Q, K, V, bm, D ** -0.5, out=out, save_lse=L)
+            res["g"] = run_block_sparse_backward(Q, K, V, out, L, dO, bm, D ** -0.5)
+        kw = {"elem_mask": O.element_mask_from_grid(grid, N, N, 64, 64)}
+    step()
+    torch.cuda.synchronize()
+    want = [t.clone() for t in (out, *res["g"])]
+    graph = _capture(step)
+    got = (out, *res["g"])                 # the graph's own output tensors
+    scratch = torch.ones(1 << 16, device="cuda")
+    for i in range(3):
+        for t in got:
+            t.zero_()
+        scratch.mul_(1.5).add_(float(i))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(got, want):
+            assert torch.equal(a, b), f"replay {i} differs from the eager step"
+    o_ref, rq, rk, rv = O.attention_grads(Q.cpu(), K.cpu(), V.cpu(), dO.cpu(), dtype=torch.float32, **kw)
+    assert (got[0].float().cpu() - o_ref).abs().max().item() <= 1.6e-2
+    for t, r in zip(got[1:], (rq, rk, rv)):
+        assert ((t.float().cpu() - r).norm() / r.norm()).item() <= 1e-2
