@@ -324,6 +324,15 @@ int plan_decode(const af_decode_args* a, size_t max_ws, DecodeParams* out, size_
   const int D = a->key.head_dim;
   int S = a->num_splits > 0 ? a->num_splits
                             : af_decode_num_splits(a->batch, a->heads_q, a->heads_kv, a->seqlen_kv, D);
+  // split length rounded up to 32 keys; empty trailing splits are dropped
+  int split_len = 0;
+  auto trim = [&]() {
+    split_len = (a->seqlen_kv + S - 1) / S;
+    split_len = (split_len + 31) & ~31;
+    S = (a->seqlen_kv + split_len - 1) / split_len;
+  };
+  trim();
+  // the limit applies to the splits that are launched, after the trim
   if (max_ws > 0) {
     const size_t per_split = af_decode_workspace_bytes(a->batch, a->heads_q, D, 1);
     const size_t fit = max_ws / per_split;
@@ -332,14 +341,13 @@ int plan_decode(const af_decode_args* a, size_t max_ws, DecodeParams* out, size_
                   per_split, max_ws);
     if ((size_t)S > fit) {
       if (a->num_splits > 0)
-        return fail(AF_ERR_WORKSPACE, "%d splits need %zu bytes of partials, above the %zu-byte limit (at most %zu)",
-                    S, per_split * S, max_ws, fit);
+        return fail(AF_ERR_WORKSPACE,
+                    "%d splits (%d non-empty) need %zu bytes of partials, above the %zu-byte limit (at most %zu)",
+                    a->num_splits, S, per_split * S, max_ws, fit);
       S = (int)fit;
+      trim();                                       // only lowers S
     }
   }
-  int split_len = (a->seqlen_kv + S - 1) / S;
-  split_len = (split_len + 31) & ~31;
-  S = (a->seqlen_kv + split_len - 1) / split_len;  // drop empty trailing splits
   *need = af_decode_workspace_bytes(a->batch, a->heads_q, D, S);
   DecodeParams& p = *out;
   memset(&p, 0, sizeof(p));
@@ -543,7 +551,9 @@ int af_decode(const af_decode_args* a, void* workspace, size_t workspace_bytes, 
 }
 
 size_t af_bwd_workspace_bytes(const af_bwd_args* args) {
-  return args == nullptr ? 0 : bwd_workspace_bytes(*args);
+  // a block-sparse launch sizes its workspace with its mask
+  if (args == nullptr || args->key.mask == AF_MASK_BLOCK_SPARSE) return 0;
+  return bwd_workspace_bytes(*args);
 }
 
 size_t af_bwd_blocksparse_workspace_bytes(const af_bwd_args* args, const af_blockmask* bm) {

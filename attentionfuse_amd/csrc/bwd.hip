@@ -141,7 +141,16 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
                !fits(a->seqlen_kv, a->k_stride[2]) || !fits(a->seqlen_kv, a->v_stride[2]) ||
                (k.rope && !fits(a->rope_len, a->rope_stride[0]))))
     return bad(AF_ERR_UNSUPPORTED, "a (batch, head) slice spans 4 GiB or more");
-  if (k.mask == AF_MASK_BLOCK_SPARSE && bm != nullptr) {
+  // the block mask is validated before the workspace size is computed from it
+  if (k.mask == AF_MASK_BLOCK_SPARSE) {
+    if (bm == nullptr || bm->full_kv_num == nullptr || bm->full_kv_idx == nullptr || bm->kv_num_blocks == nullptr ||
+        bm->kv_indices == nullptr || bm->q_num_blocks == nullptr || bm->q_indices == nullptr)
+      return bad(AF_ERR_BAD_ARG, "block-sparse backward needs the Q-major and K-major block lists");
+    if ((bm->block_m != 64 && bm->block_m != 128) || (bm->block_n != 64 && bm->block_n != 128))
+      return bad(AF_ERR_UNSUPPORTED, "block-sparse backward supports 64 or 128 blocks");
+    if (bm->n_q_blocks != (a->seqlen_q + bm->block_m - 1) / bm->block_m ||
+        bm->n_kv_blocks != (a->seqlen_kv + bm->block_n - 1) / bm->block_n)
+      return bad(AF_ERR_BAD_ARG, "block mask grid does not match the sequence lengths");
     if (bm->q_items != nullptr &&
         (rc = check_plan(bm->n_q_items, bm->q_splits, bm->n_q_splits, bm->n_q_slots, bm->n_q_blocks, "q")))
       return rc;
@@ -229,14 +238,6 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   g.waves_kv = 4;
   g.waves_q = 4;
   if (k.mask == AF_MASK_BLOCK_SPARSE) {
-    if (bm == nullptr || bm->full_kv_num == nullptr || bm->full_kv_idx == nullptr || bm->kv_num_blocks == nullptr ||
-        bm->kv_indices == nullptr || bm->q_num_blocks == nullptr || bm->q_indices == nullptr)
-      return bad(AF_ERR_BAD_ARG, "block-sparse backward needs the Q-major and K-major block lists");
-    if ((bm->block_m != 64 && bm->block_m != 128) || (bm->block_n != 64 && bm->block_n != 128))
-      return bad(AF_ERR_UNSUPPORTED, "block-sparse backward supports 64 or 128 blocks");
-    if (bm->n_q_blocks != (a->seqlen_q + bm->block_m - 1) / bm->block_m ||
-        bm->n_kv_blocks != (a->seqlen_kv + bm->block_n - 1) / bm->block_n)
-      return bad(AF_ERR_BAD_ARG, "block mask grid does not match the sequence lengths");
     if (const int rc = check_elem_masks(bm, k.head_dim)) return rc;
     g.waves_kv = bm->block_n / 32;
     g.waves_q = bm->block_m / 32;

@@ -411,8 +411,10 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
       const int32_t* it = p.bs_kv_items + 4 * kbi;
       kb = it[0];
       bs_e0 = it[1];
-      bs_ne = it[2];
       bs_slot = it[3];
+      // a whole list (slot -1) is walked to its current count on the
+      // device, so lists edited in place keep their plan valid
+      bs_ne = bs_slot >= 0 ? it[2] : -1;
     }
   }
   const int split = rem / BHK;
@@ -460,7 +462,8 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
     bs_sub = p.bs_block_m / 32;
     bs_n = p.bs_q_num[kb];
     bs_row = p.bs_q_idx + kb * p.bs_q_rs;
-    ntq = (bs_ne >= 0 ? bs_ne : bs_n) * bs_sub;
+    // a piece of a split list stops at the list's current end
+    ntq = (bs_ne >= 0 ? min(bs_ne, max(bs_n - bs_e0, 0)) : bs_n) * bs_sub;
   } else {
     ntq = m_hi > m_lo ? (m_hi - m_lo + 31) / 32 : 0;
   }
@@ -793,8 +796,8 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
       const int32_t* it = p.bs_q_items + 4 * mbi;
       mb = it[0];
       bs_e0 = it[1];
-      bs_ne = it[2];
       bs_slot = it[3];
+      bs_ne = bs_slot >= 0 ? it[2] : -1;
     }
   }
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.G;
@@ -829,7 +832,7 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
     bs_npart = p.bs_part_num[mb];
     bs_full_row = p.bs_full_idx + mb * p.bs_full_rs;
     bs_part_row = p.bs_part_idx + mb * p.bs_part_rs;
-    ntiles = (bs_ne >= 0 ? bs_ne : bs_nfull + bs_npart) * bs_sub;
+    ntiles = (bs_ne >= 0 ? min(bs_ne, max(bs_nfull + bs_npart - bs_e0, 0)) : bs_nfull + bs_npart) * bs_sub;
   } else {
     ntiles = n_hi > n_lo ? (n_hi - n_lo + 31) / 32 : 0;
   }

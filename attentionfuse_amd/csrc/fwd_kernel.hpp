@@ -27,6 +27,9 @@
 //    exceeds it by more than 2^kTau, so the O rescale is rare.
 //  * Q stays in registers for the whole kernel, rotated once.
 //  * causal grids run the longest query blocks first.
+//  * ALiBi and block-sparse kernels defer P V by one step (fwd_defer): the
+//    score MFMAs of tile t+1 and the P V MFMAs of tile t-1 alternate, one
+//    per chunk, with the softmax VALU work of tile t in one basic block.
 #pragma once
 
 #include "af_common.hpp"
@@ -79,20 +82,39 @@ struct FwdParams {
   int32_t window;
 };
 
+// Whether a forward instantiation runs the deferred P V pipeline (see the
+// kernel): lazy softmax kernels with head dims up to 64 that already run two
+// waves per SIMD (ALiBi) or walk a block mask.  Measured on MI355X (same-box
+// A/B, config 2's shape): ALiBi 1-2 % and the BigBird forward 2-3 % faster;
+// the causal kernel without a bias, which otherwise runs three waves per
+// SIMD, 3-4 % slower at the deferred pipeline's two.
+#ifndef AF_FWD_DEFER
+#define AF_FWD_DEFER 1
+#endif
+template <int D, int MASK, int BIAS, int NORM>
+constexpr bool fwd_defer() {
+  if (!AF_FWD_DEFER || D > 64 || NORM != NORM_SOFTMAX) return false;
+  if (MASK == MASK_BS || MASK == MASK_BSE) return BIAS != BIAS_ALIBI;
+  // ALiBi is lazy where its walk makes the bias fall from tile to tile
+  return BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW || MASK == MASK_FULL);
+}
+
 // Waves per SIMD the register budget is set for: head dims up to 64 fit
 // 168 VGPRs (three waves), except ALiBi: the causal-type kind's initial
 // score accumulator takes 16 more, and the dense kind's lazy steps spilled
-// 300 registers' worth at three waves (two waves); D = 128 takes one.
-template <int D, int MASK, int BIAS>
+// 300 registers' worth at three waves (two waves); D = 128 takes one.  The
+// deferred pipeline keeps two score tiles and two P tiles live (two waves).
+template <int D, int MASK, int BIAS, int NORM>
 constexpr int fwd_waves_per_eu() {
   if (D > 64) return 1;
+  if (fwd_defer<D, MASK, BIAS, NORM>()) return 2;
   return (BIAS == BIAS_ALIBI && MASK != MASK_SW && MASK != MASK_BS && MASK != MASK_BSE) ? 2 : 3;
 }
 
 // Head dims up to 64 fit in 168 VGPRs (a few setup values spill outside the
 // loop): three waves per SIMD, three 4-wave workgroups per CU.
 template <class E, int D, int MASK, int BIAS, int NORM, bool ROPE, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(fwd_waves_per_eu<D, MASK, BIAS>())))
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(fwd_waves_per_eu<D, MASK, BIAS, NORM>())))
     fwd_kernel(const FwdParams p) {
   constexpr int NT = WAVES * 64;
   constexpr int BM = 32 * WAVES;
@@ -102,7 +124,9 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   constexpr int TILE = BN * D;       // one swizzled (BN x D) tile, no padding
 
   // two K slots, then two V slots
-  __shared__ __attribute__((aligned(16))) uint16_t lds[4 * TILE];
+  constexpr bool kDefer = fwd_defer<D, MASK, BIAS, NORM>();
+  constexpr int kSlots = 2;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kSlots * TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -126,8 +150,10 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
       const int32_t* it = p.bs_items + 4 * mbi;
       mb = it[0];
       bs_e0 = it[1];
-      bs_ne = it[2];
       bs_slot = it[3];
+      // a whole list (slot -1) is walked to its current count on the
+      // device, so lists edited in place keep their plan valid
+      bs_ne = bs_slot >= 0 ? it[2] : -1;
     }
   }
   const int b = bh / p.Hq;
@@ -188,7 +214,8 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     bs_npart = p.bs_part_num[mb];
     bs_full_row = p.bs_full_idx + mb * p.bs_full_rs;
     bs_part_row = p.bs_part_idx + mb * p.bs_part_rs;
-    ntiles = (bs_ne >= 0 ? bs_ne : bs_nfull + bs_npart) * bs_sub;
+    // a piece of a split list stops at the list's current end
+    ntiles = (bs_ne >= 0 ? min(bs_ne, max(bs_nfull + bs_npart - bs_e0, 0)) : bs_nfull + bs_npart) * bs_sub;
   } else {
     ntiles = n_hi > n_lo ? (n_hi - n_lo + BN - 1) / BN : 0;
   }
@@ -237,7 +264,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // slot parity t & 1 is passed as a literal by the unrolled pipeline so
   // that every LDS address is a register plus an immediate offset
   auto load_k = [&](int t, int par) { kdma.load(lds, par * TILE, w, kbase, kstr, p.Nkv, tile_n0(t)); };
-  auto load_v = [&](int t, int par) { vdma.load(lds, (2 + par) * TILE, w, vbase, vstr, p.Nkv, tile_n0(t)); };
+  auto load_v = [&](int t, int par) { vdma.load(lds, (kSlots + par) * TILE, w, vbase, vstr, p.Nkv, tile_n0(t)); };
   // per-lane LDS offsets: the K rows of the S^T MFMA (key block 0; block 1 is
   // 32 rows on, same swizzle) and the transposed V reads of the P V MFMA
   int koff[KS];
@@ -550,7 +577,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
 
   // O += P V(t), V^T read transposed from its LDS slot.
   auto pv = [&](int par, const u32x4* pf) {
-    const uint16_t* Vs = lds + (2 + par) * TILE;
+    const uint16_t* Vs = lds + (kSlots + par) * TILE;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
@@ -574,7 +601,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   constexpr int kVAhead = kVOps < AF_FWD_V_AHEAD(D) ? kVOps : AF_FWD_V_AHEAD(D);
   auto read_vop = [&](int par, int i) -> u32x4 {
     const int kk = i / DB, db = i % DB;
-    const uint16_t* vt = lds + (2 + par) * TILE + 16 * kk * D;
+    const uint16_t* vt = lds + (kSlots + par) * TILE + 16 * kk * D;
     const u32x2 lo = lds_read_tr16(vt + voff[db][0]);
     const u32x2 hi = lds_read_tr16(vt + voff[db][1]);
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
@@ -660,6 +687,82 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     }
   };
 
+  // ---- deferred P V: one interleaved instruction stream per step ------------
+  // Step t of the deferred pipeline runs the score MFMAs of tile t+1 and the
+  // P V MFMAs of tile t-1 (P(t-1) kept packed from the previous step) while
+  // the VALU computes P of tile t.  All three are independent, so the step
+  // is one basic block in which every MFMA is followed by its share of the
+  // softmax: a fused multiply-add, an exponential, a convert and a row-sum
+  // dot of one packed pair, each pair's three stages one chunk apart, and
+  // the LDS operand reads kOpAhead MFMAs ahead.  The scheduling barriers fix
+  // that order.  Without them the lazy test (below) splits each step into
+  // a VALU-only run before it and an MFMA-only run of P V after it.
+  constexpr int kSM = 2 * KS;            // score MFMAs per tile
+  constexpr int kPM = DB * (BN / 16);    // P V MFMAs per tile (== kSM)
+  constexpr int kPairs = BN / 4;         // packed P pairs per lane and tile
+  static_assert(kSM == kPM, "score and P V MFMAs alternate");
+#ifndef AF_FWD_OP_AHEAD
+#define AF_FWD_OP_AHEAD 4
+#endif
+  constexpr int kOpAhead = AF_FWD_OP_AHEAD;
+  // operand of score MFMA j: key block j % 2, k-step j / 2
+  auto read_sop = [&](int par, int j) -> u32x4 {
+    return ld16(lds + par * TILE + 32 * (j & 1) * D + koff[j >> 1]);
+  };
+  // S(t+1) into nxt (key slot kpar), with PV: O += P(t-1) V(t-1) (value slot
+  // vpar, P in pprev); P(t) of the scores s under lg into pf.  Returns the
+  // fp32 sum of this lane's 32 rounded P of tile t.
+  auto mix = [&](auto pv_on, int kpar, int vpar, f32x16* s, const Logit& lg, f32x16* nxt,
+                 const u32x4* pprev, u32x4* pf) -> float {
+    constexpr bool PV = decltype(pv_on)::value;
+    constexpr int M = PV ? kSM + kPM : kSM;
+    constexpr int A = M < kOpAhead ? M : kOpAhead;
+    // MFMA i: with PV even i is score MFMA i/2 and odd i P V MFMA i/2
+    auto read_op = [&](int i) -> u32x4 {
+      if (PV && (i & 1)) return read_vop(vpar, i >> 1);
+      return read_sop(kpar, PV ? i >> 1 : i);
+    };
+    u32x4 op[M];
+    float ts[4];
+#pragma unroll
+    for (int i = 0; i < A; ++i) op[i] = read_op(i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < M + 2; ++c) {
+      if (c < M) {
+        if (PV && (c & 1)) {
+          const int j = c >> 1;
+          o[j % DB] = E::mfma32(op[c], pprev[j / DB], o[j % DB]);
+        } else {
+          const int j = PV ? c >> 1 : c;
+          const int kb = j & 1, ks = j >> 1;
+          nxt[kb] = E::mfma32(op[c], qf[ks], ks == 0 ? sinit : nxt[kb]);
+        }
+      }
+      if (c + A < M) op[c + A] = read_op(c + A);
+#pragma unroll
+      for (int p = 0; p < kPairs; ++p) {
+        const int cp = p * M / kPairs;      // chunk of the pair's first stage
+        const int kb = p >> 3, r = 2 * (p & 7);
+        if (c == cp) {
+          s[kb][r] = __builtin_fmaf(s[kb][r], lg.zc, lg.off[kb]);
+          s[kb][r + 1] = __builtin_fmaf(s[kb][r + 1], lg.zc, lg.off[kb]);
+        } else if (c == cp + 1) {
+          s[kb][r] = __builtin_amdgcn_exp2f(s[kb][r]);
+          s[kb][r + 1] = __builtin_amdgcn_exp2f(s[kb][r + 1]);
+        } else if (c == cp + 2) {
+          const uint32_t w2 = E::pack(s[kb][r], s[kb][r + 1]);
+          pf[2 * kb + (r >> 3)][(r & 7) >> 1] = w2;
+          if (p < 4) E::dot_first(w2, ts[p & 3]);
+          else E::dot_pair(w2, ts[p & 3]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    E::sums_ready(ts[0], ts[1], ts[2], ts[3]);
+    return (ts[0] + ts[1]) + (ts[2] + ts[3]);
+  };
+
   // ---- software pipeline ---------------------------------------------------
   // Iteration t issues the loads of K(t+2) and V(t+1), masks tile t (and for
   // an exact step updates the running max), then runs the score MFMAs of
@@ -669,9 +772,10 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // last read by the score MFMAs of iteration t-1; V(t+1) overwrites V(t-1),
   // last read in iteration t-1; the barrier closing each iteration separates
   // the two.
+  // The deferred pipeline (below) loads V(t) in step t instead.
   if (ntiles > 0) {
     load_k(0, 0);
-    load_v(0, 0);
+    if constexpr (!kDefer) load_v(0, 0);
   }
   if (ntiles > 1) load_k(1, 1);
   wait_lds_dma();
@@ -700,7 +804,53 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // Causal-type ALiBi walks away from the query (kDescend) and two-sided
   // ALiBi outwards from it (kOutward), so ALiBi steps are lazy like the rest.
   constexpr bool kLazy = NORM == NORM_SOFTMAX && (BIAS != BIAS_ALIBI || kDescend || kOutward);
-  if constexpr (kLazy) {
+  static_assert(!kDefer || kLazy, "the deferred pipeline takes lazy steps");
+  if constexpr (kDefer) {
+    // Step t loads K(t+2) into K slot t & 1 and V(t) into V slot t & 1, reads
+    // K(t+1) and V(t-1) from the other slots, and the P V of the last tile
+    // follows the loop.  Slot reuse: K slot t & 1 held K(t), last read by
+    // the score MFMAs of step t-1; V slot t & 1 held V(t-2), last read by the
+    // P V of step t-1; the barrier closing step t-1 separates them.
+    auto issue_d = [&](int t, int par) {
+      if (t + 2 < ntiles) load_k(t + 2, par);
+      load_v(t, par);
+    };
+    using no_pv = std::integral_constant<bool, false>;
+    using with_pv = std::integral_constant<bool, true>;
+    u32x4 pa[BN / 16], pb[BN / 16];
+    // step t >= 1 of parity par: P V(t-1) with pprev, P(t) into pf
+    auto step_d = [&](int t, int par, f32x16* s, f32x16* nxt, const u32x4* pprev, u32x4* pf) {
+      issue_d(t, par);
+      const Logit lg0 = bias_mask(t, s, true);
+      Logit lg = lg0;
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb) lg.off[kb] -= m_run;
+      float tsum = mix(with_pv{}, par ^ 1, par ^ 1, s, lg, nxt, pprev, pf);
+      if (__builtin_amdgcn_ballot_w64(!(tsum < kRedo)) != 0) {
+        scores_global(t, s);
+        const Logit lg1 = rebase(s, bias_mask(t, s, false));
+        softmax_tile(s, lg1, pf);
+        tsum = tile_rowsum(pf);
+      }
+      lsum[0] += tsum;
+      close();
+    };
+    if (ntiles > 0) {
+      issue_d(0, 0);
+      const Logit lg = rebase(sa, bias_mask(0, sa, true));
+      lsum[0] += mix(no_pv{}, 1, 1, sa, lg, sb, pb, pa);
+      close();
+    }
+    for (int t = 1; t < ntiles; t += 2) {
+      step_d(t, 1, sb, sa, pa, pb);
+      if (t + 1 < ntiles) step_d(t + 1, 0, sa, sb, pb, pa);
+    }
+    if (ntiles > 0) {
+      // P(ntiles-1) is in pa for an even tile index, pb for an odd one
+      if ((ntiles - 1) & 1) pv_pipe(1, pb);
+      else pv_pipe(0, pa);
+    }
+  } else if constexpr (kLazy) {
     if (ntiles > 0) {
       issue(0, 0);
       step_exact(0, 0, sa, sb);

@@ -32,16 +32,31 @@ def can_backward(graph: Graph) -> bool:
 
 # Backward launch override, the counterpart of the reference's _BWD_TILE
 # (reference: attnfuse/runtime/backward.py:18-47).  On gfx950 the block
-# shapes are fixed per instantiation (128-row dQ and 128-key dK/dV
-# workgroups, or the BlockMask's blocks); the runtime choice is how many
-# dK/dV workgroups split one key block's GQA query heads.  With "auto" the
-# library picks it (``_pick_backward_tile``); otherwise "group_split" (a
-# power of two dividing H_q / H_kv) is used as given, e.g.
+# shapes and pipeline depths are fixed per instantiation (128-row dQ and
+# 128-key dK/dV workgroups of four waves for 16-bit inputs, or the
+# BlockMask's blocks); the runtime choice is how many dK/dV workgroups split
+# one key block's GQA query heads.  With "auto" the library picks it
+# (``_pick_backward_tile``); otherwise "group_split" (a power of two dividing
+# H_q / H_kv) is used as given, e.g.
 #     backward._BWD_TILE.update({"auto": False, "group_split": 2})
+# The reference's own keys are kept: None means the launch's own value, and
+# with "auto" off a set BLOCK_M / BLOCK_N / num_warps must equal the shape the
+# launch uses; any other value, and any num_stages, raises ValueError rather
+# than being silently ignored.
 _BWD_TILE = {
+    "BLOCK_M": None,
+    "BLOCK_N": None,
+    "num_warps": None,
+    "num_stages": None,
     "group_split": 0,
     "auto": True,
 }
+_REFERENCE_KEYS = ("BLOCK_M", "BLOCK_N", "num_warps", "num_stages")
+
+# The dense 16-bit launch shape: what _pick_backward_tile(N_q) reports, the
+# reference's call form, which knows only the sequence length.
+_DEFAULT_TILE = {"BLOCK_M": 128, "BLOCK_N": 128, "num_warps": 4,
+                 "num_stages": None, "group_split": 0}
 
 
 def _group_split_request() -> int:
@@ -50,15 +65,49 @@ def _group_split_request() -> int:
     return int(_BWD_TILE.get("group_split", 0) or 0)
 
 
-def _pick_backward_tile(args: "N.BwdArgsC", block_mask=None) -> dict:
-    """The backward launch shape for these packed arguments, as the library
-    will use it: {"BLOCK_M", "BLOCK_N", "group_split"}."""
+def _pick_backward_tile(args, block_mask=None) -> dict:
+    """The backward launch shape: {"BLOCK_M", "BLOCK_N", "num_warps",
+    "num_stages", "group_split"}.
+
+    ``args`` is either the packed ``BwdArgsC`` of a launch (the shape the
+    library will use for it, group split included) or, as in the reference
+    (attnfuse/runtime/backward.py:35), the query length N_q: then the dense
+    16-bit shape, whose block sizes do not depend on N_q on gfx950, and
+    group_split 0 (chosen per launch).  num_stages is None: the pipeline
+    depth is fixed by the instantiation."""
+    if not isinstance(args, N.BwdArgsC):
+        int(args)                       # the reference passes N_q
+        return dict(_DEFAULT_TILE)
     import ctypes as C
     bm, bn, gs = C.c_int32(), C.c_int32(), C.c_int32()
     c_bm = block_mask._c() if block_mask is not None else None
     N.check(N.lib().af_bwd_tile(args, c_bm, C.byref(bm), C.byref(bn),
                                 C.byref(gs)))
-    return {"BLOCK_M": bm.value, "BLOCK_N": bn.value, "group_split": gs.value}
+    return {"BLOCK_M": bm.value, "BLOCK_N": bn.value,
+            "num_warps": bm.value // 32, "num_stages": None,
+            "group_split": gs.value}
+
+
+def _check_tile_request(args, block_mask=None) -> None:
+    """Raise ValueError when _BWD_TILE (with "auto" off) asks for a reference
+    key value this launch cannot honour."""
+    if _BWD_TILE.get("auto", True):
+        return
+    want = {k: _BWD_TILE[k] for k in _REFERENCE_KEYS
+            if _BWD_TILE.get(k) is not None}
+    if not want:
+        return
+    have = _pick_backward_tile(args, block_mask)
+    bad = sorted(k for k, v in want.items()
+                 if k == "num_stages" or have.get(k) != v)
+    if bad:
+        raise ValueError(
+            f"_BWD_TILE sets {', '.join(f'{k}={want[k]}' for k in bad)}, "
+            f"which the gfx950 backward cannot use: its block shape is fixed "
+            f"per instantiation (this launch: BLOCK_M={have['BLOCK_M']}, "
+            f"BLOCK_N={have['BLOCK_N']}, num_warps={have['num_warps']}) and "
+            f"its pipeline depth is not selectable; only 'group_split' can "
+            f"be chosen")
 
 
 def _bwd_workspace(device, nbytes: int) -> torch.Tensor:
@@ -105,6 +154,7 @@ def _run_backward_key(key, Q, K, V, O, L, dO, sm_scale, window, cos, sin,
     a.scale = float(sm_scale)
     a.window = int(window or 0)
     a.group_split = _group_split_request()
+    _check_tile_request(a, block_mask)
     bm = block_mask._c() if block_mask is not None else None
     nbytes = int(N.lib().af_bwd_workspace_bytes(a) if bm is None else
                  N.lib().af_bwd_blocksparse_workspace_bytes(a, bm))

@@ -94,7 +94,11 @@ class BlockMask:
     n_active: int
     n_full: int
     # work plan of the split walks; made from the list lengths on first use
-    # when the mask was not built by block_mask_from_blocks
+    # when the mask was not built by block_mask_from_blocks.  A list the plan
+    # keeps whole is walked to its current device-side count, so lists may be
+    # edited in place (e.g. between graph replays); a list the plan splits
+    # into pieces is walked by those pieces, clamped to its current count:
+    # after changing such a list's length, call plan_work() again.
     plan: Optional[BlockMaskPlan] = field(default=None, repr=False,
                                           compare=False)
     # element masks of the partial tiles (create_block_mask(exact=True)):

@@ -91,7 +91,11 @@ typedef struct af_blockmask {
    * NULL / 0: one workgroup per query block and per key block, the
    * reference's grid).  q_*: the Q-major lists (forward, dQ); kv_*: the
    * K-major lists (dK/dV).  An item is (list, first entry, entries, partial
-   * slot or -1); a split is (list, first slot, slots). */
+   * slot or -1); a split is (list, first slot, slots).  An item with slot -1
+   * is a whole list and is walked to the list's count in device memory at
+   * launch time, so lists may be rewritten in place between launches (graph
+   * replays included); the pieces of a split list are clamped to that count,
+   * and a plan must be remade after a split list changes length. */
   const int32_t* q_items;   /* (n_q_items, 4)   */
   const int32_t* q_splits;  /* (n_q_splits, 3)  */
   const int32_t* kv_items;  /* (n_kv_items, 4)  */
@@ -216,12 +220,15 @@ int af_decode(const af_decode_args* args, void* workspace,
  * hipMalloc).  The split partials live in a library-owned device array of
  * AF_DECODE_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on that
  * GPU until the process ends.  With num_splits <= 0 the split count is
- * lowered until the partials fit; an explicit num_splits, or a batch whose
- * single-split partials (B * H_q * (2 + D) * 4 bytes) do not fit, returns
- * AF_ERR_WORKSPACE.  Every call on one GPU shares the array: calls that
- * overlap in time on one GPU (other streams, other threads) race; calls on
- * one stream are ordered.  Results equal af_decode's for the same split
- * count. */
+ * lowered until the partials fit; an explicit num_splits whose non-empty
+ * splits (after the 32-key rounding of the split length) do not fit, or a
+ * batch whose single-split partials (B * H_q * (2 + D) * 4 bytes) do not
+ * fit, returns AF_ERR_WORKSPACE.  Every call on one GPU shares the array:
+ * calls that overlap in time on one GPU (other streams, other threads) race;
+ * calls on one stream are ordered.  Results equal af_decode's for the same
+ * split count.  The first call on a GPU looks up the array's device address
+ * (hipGetSymbolAddress); make it before capturing a graph that calls this
+ * function, after which captured calls record only the two kernel launches. */
 #define AF_DECODE_NOALLOC_SCRATCH_BYTES (4u << 20)
 int af_decode_noalloc(const af_decode_args* args, void* stream);
 
@@ -258,7 +265,9 @@ typedef struct af_bwd_args {
  * delta (an fp32 pair per query row); with fused RoPE the rotated q~ and k~ in the input dtype; and when
  * the query heads of a GQA group are split over several dK/dV workgroups
  * (grids of at most two workgroups per CU), fp32 dK and dV partial sums
- * per split. */
+ * per split.  Returns 0 for a block-sparse key (key.mask
+ * AF_MASK_BLOCK_SPARSE): its workspace depends on the mask's work plan, so
+ * such callers use af_bwd_blocksparse_workspace_bytes. */
 size_t af_bwd_workspace_bytes(const af_bwd_args* args);
 /* fp16 / bf16, or AF_F32 (fp32 throughout on the fp32 MFMAs, head dims 32,
  * 64, 128).  Block-sparse (key.mask AF_MASK_BLOCK_SPARSE) needs bm with

@@ -222,3 +222,10 @@ def test_element_mask_arguments_are_checked_before_any_launch():
     ws = int(lib.af_bwd_blocksparse_workspace_bytes(b, bm))
     assert lib.af_bwd(b, bm, 256, ws, None) == N.AF_ERR_BAD_ARG
     assert "all NULL or all set" in N.last_error()
+    # a block-sparse key has no mask-free workspace size, and a bad block
+    # size is reported as such before any workspace arithmetic uses it
+    assert int(lib.af_bwd_workspace_bytes(b)) == 0
+    bm.q_col_bits = bm.part_row_bits = None
+    bm.block_m = 96
+    assert lib.af_bwd(b, bm, None, 0, None) == N.AF_ERR_UNSUPPORTED
+    assert "64 or 128 blocks" in N.last_error()

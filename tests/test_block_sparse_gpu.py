@@ -173,3 +173,41 @@ def test_head_dim_256_forward_and_backward(dtype):
     assert (out.detach().float().cpu() - o_ref).abs().max().item() <= TOL[dtype]
     for got, ref in ((q.grad, dq), (k.grad, dk), (v.grad, dv)):
         assert ((got.float().cpu() - ref).norm() / ref.norm()).item() <= GRAD_REL
+
+
+def test_lists_edited_in_place_between_launches():
+    """A mask whose lists are rewritten in place on the device (as between
+    graph replays) is walked to its new lengths without remaking the work
+    plan: whole (unsplit) lists take their counts from the device.  Grid A
+    has rows and columns of 2 or 3 tiles, grid B of 3 everywhere, with the
+    same padded widths; B's lists are copied into A's tensors and the same
+    BlockMask object is launched again."""
+    from attnfuse.runtime.block_mask import run_block_sparse_backward
+    print("[bs] lists edited in place", flush=True)
+    Nn, nb = 512, 8
+    r = torch.arange(nb)
+    grid_a = (r[:, None] - r[None, :]).abs() <= 1
+    grid_b = torch.zeros(nb, nb, dtype=torch.bool)
+    for i in range(nb):
+        grid_b[i, [i, (i + 2) % nb, (i + 5) % nb]] = True
+    bm = block_mask_from_blocks(grid_a, 64, 64, device="cuda")
+    bm_b = block_mask_from_blocks(grid_b, 64, 64, device="cuda")
+    assert bm.plan.q_splits.shape[0] == 0 and bm.plan.kv_splits.shape[0] == 0
+    fields = ("full_kv_num", "full_kv_idx", "q_num_blocks", "q_indices", "kv_num_blocks", "kv_indices")
+    for f in fields:
+        assert getattr(bm, f).shape == getattr(bm_b, f).shape, f
+    Q, K, V, dO = make(1, 2, Nn, D, torch.float16, seed=5)
+    for grid in (grid_a, grid_b):
+        if grid is grid_b:
+            for f in fields:
+                getattr(bm, f).copy_(getattr(bm_b, f))
+        lse = torch.empty(Q.shape[:3], device="cuda", dtype=torch.float32)
+        out = run_block_sparse(Q, K, V, bm, D ** -0.5, save_lse=lse)
+        dq, dk, dv = run_block_sparse_backward(Q, K, V, out, lse, dO, bm, D ** -0.5)
+        torch.cuda.synchronize()
+        em = elem_mask(grid, Nn)
+        o_ref, rq, rk, rv = O.attention_grads(Q.cpu(), K.cpu(), V.cpu(), dO.cpu(), dtype=torch.float64,
+                                              elem_mask=em)
+        assert (out.double().cpu() - o_ref).abs().max().item() <= TOL[torch.float16]
+        for got, ref in ((dq, rq), (dk, rk), (dv, rv)):
+            assert ((got.double().cpu() - ref).norm() / ref.norm()).item() <= GRAD_REL

@@ -284,6 +284,48 @@ def test_backward_tile_override_reaches_the_library():
     assert bwd._group_split_request() == 0
 
 
+def test_backward_tile_reference_keys():
+    """The reference's _BWD_TILE keys (attnfuse/runtime/backward.py:26-32)
+    and its _pick_backward_tile(N_q) call form: a key that matches the
+    launch's shape is accepted, any other value -- and any num_stages --
+    raises ValueError instead of being ignored; with "auto" on the keys are
+    not consulted, as in the reference."""
+    from attentionfuse_amd.runtime import _native as N
+    from attentionfuse_amd.runtime import backward as bwd
+    ref = bwd._pick_backward_tile(4096)
+    assert {"BLOCK_M", "BLOCK_N", "num_warps", "num_stages"} <= set(ref)
+    assert (ref["BLOCK_M"], ref["BLOCK_N"], ref["num_warps"]) == (128, 128, 4)
+    assert bwd._pick_backward_tile(256) == ref
+    a = N.BwdArgsC()
+    a.key = N.SpecKeyC(0, 64, 1, 0, 0, 0)
+    a.batch, a.heads_q, a.heads_kv, a.seqlen_q, a.seqlen_kv = 1, 12, 12, 4096, 4096
+    have = bwd._pick_backward_tile(a)
+    assert (have["BLOCK_M"], have["BLOCK_N"], have["num_warps"]) == (128, 128, 4)
+    saved = dict(bwd._BWD_TILE)
+    try:
+        # the reference sweep's form: update with a config, then auto off
+        bwd._BWD_TILE.update({"BLOCK_M": 64, "BLOCK_N": 64, "num_warps": 4})
+        bwd._check_tile_request(a)          # auto still on: not consulted
+        bwd._BWD_TILE["auto"] = False
+        with pytest.raises(ValueError, match="BLOCK_M=64"):
+            bwd._check_tile_request(a)
+        bwd._BWD_TILE.update({"BLOCK_M": 128, "BLOCK_N": 128, "num_warps": 4})
+        bwd._check_tile_request(a)          # the launch's own shape
+        bwd._BWD_TILE["num_warps"] = 8
+        with pytest.raises(ValueError, match="num_warps=8"):
+            bwd._check_tile_request(a)
+        bwd._BWD_TILE.update({"num_warps": None, "num_stages": 2})
+        with pytest.raises(ValueError, match="num_stages=2"):
+            bwd._check_tile_request(a)
+        bwd._BWD_TILE.update({"BLOCK_M": None, "BLOCK_N": None, "num_stages": None,
+                              "group_split": 2})
+        bwd._check_tile_request(a)
+        assert bwd._group_split_request() == 2
+    finally:
+        bwd._BWD_TILE.clear()
+        bwd._BWD_TILE.update(saved)
+
+
 def test_constexprs_change_with_variant():
     @af.attention
     def dense(Q, K, V):

@@ -46,6 +46,24 @@ def test_cross_attention_dense(Nq, Nkv):
     assert run_case("dense", 2, 4, 2, Nq, 64, F32, Nkv=Nkv) <= TOL
 
 
+def test_config1_exact_shape():
+    """BASELINE config 1 as written -- GPT-2-small causal forward, B=1 H=12
+    N=512 D=64 fp32, Q/K/V ~ N(0,1) drawn from seed 0 in that order (the
+    draw bench.py's CPU leg times), scale 1/sqrt(64) -- on the fp32 HIP
+    kernel, against the oracle on the same tensors."""
+    print("[fwd f32] config 1 B1 H12 N512 D64 causal", flush=True)
+    g = torch.Generator().manual_seed(0)
+    Qc, Kc, Vc = (torch.randn(1, 12, 512, 64, generator=g) for _ in range(3))
+    out = af.attention(variant("causal", 12))(Qc.cuda(), Kc.cuda(), Vc.cuda())
+    torch.cuda.synchronize()
+    assert out.shape == (1, 12, 512, 64) and out.dtype == F32
+    want = O.naive_attention(Qc, Kc, Vc, causal=True)
+    err = (out.cpu() - want).abs().max().item()
+    assert err <= TOL, err
+    # and at the reference's own fp32 tolerance (tests/test_correctness.py:28-38)
+    assert torch.allclose(out.cpu(), want, atol=2e-3, rtol=0)
+
+
 def test_reference_dense_case():
     """The reference's fp32 test_dense (tests/test_correctness.py:28-38) at
     its own tolerance, and at this kernel's."""

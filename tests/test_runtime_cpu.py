@@ -116,3 +116,21 @@ def test_call_keywords_are_checked_before_any_launch():
     zq = z.clone().requires_grad_(True)
     with pytest.raises(ValueError):
         causal(zq, z, z, out=torch.empty_like(z))
+
+
+def test_missing_library_raises_runtime_error(monkeypatch, tmp_path):
+    """Failure detection: a library that is not built, or is not a shared
+    object, makes the first native call raise RuntimeError naming the path
+    (there is no CPU fallback to drop into)."""
+    from attentionfuse_amd.runtime import _native as N
+    missing = tmp_path / "libattnfuse_hip.so"
+    monkeypatch.setattr(N, "_lib", None)
+    monkeypatch.setenv("ATTNFUSE_LIB", str(missing))
+    with pytest.raises(RuntimeError, match="not built"):
+        N.lib()
+    with pytest.raises(RuntimeError, match="not built"):
+        N.last_error()
+    missing.write_bytes(b"not an ELF file")
+    with pytest.raises(RuntimeError, match="cannot load"):
+        N.lib()
+    assert N._lib is None                  # nothing half-loaded is cached

@@ -5,7 +5,8 @@ The two entry points launch the same kernels with the same split count, so
 their outputs must agree bit for bit; both are also checked against the fp32
 oracle.  Two calls run back to back, the second on a smaller problem, so the
 shared device array is reused with a different layout.  The split-count
-fitting and the size limit are checked too."""
+fitting and the size limit are checked too, and a call captured in a graph
+(after the first, eager call on the GPU) replays bit-identically."""
 import ctypes as C
 
 import pytest
@@ -113,12 +114,27 @@ def test_alibi_after_a_larger_call():
 
 def test_sizes_beyond_the_limit_are_refused():
     lib = N.lib()
-    Q, K, V = _make(1, 8, 2, 4096, 128, torch.bfloat16, 0)
-    out = torch.empty_like(Q)
-    stream = torch.cuda.current_stream().cuda_stream
-    # explicit split count whose partials exceed the array
     per = int(lib.af_decode_workspace_bytes(1, 8, 128, 1))
     too_many = LIMIT // per + 1
+    stream = torch.cuda.current_stream().cuda_stream
+    # an explicit split count above the limit that the 32-key split rounding
+    # trims to 128 non-empty splits is accepted, and matches af_decode
+    print(f"[noalloc] {too_many} splits of 4096 keys", flush=True)
+    Q, K, V = _make(1, 8, 2, 4096, 128, torch.bfloat16, 0)
+    o_na = torch.full_like(Q, float("nan"))
+    N.check(lib.af_decode_noalloc(_args(Q, K, V, o_na, too_many), stream))
+    o_ref = torch.full_like(Q, float("nan"))
+    nbytes = int(lib.af_decode_workspace_bytes(1, 8, 128, too_many))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    N.check(lib.af_decode(_args(Q, K, V, o_ref, too_many), ws.data_ptr(), nbytes, stream))
+    torch.cuda.synchronize()
+    assert torch.equal(o_na, o_ref)
+    # one whose non-empty splits still exceed the array is refused: 32-key
+    # splits of a cache 32 * too_many keys long
+    n_kv = 32 * too_many
+    print(f"[noalloc] {too_many} splits of {n_kv} keys (refused)", flush=True)
+    Q, K, V = _make(1, 8, 2, n_kv, 128, torch.bfloat16, 0)
+    out = torch.empty_like(Q)
     assert lib.af_decode_noalloc(_args(Q, K, V, out, too_many), stream) == N.AF_ERR_WORKSPACE
     assert "limit" in N.last_error()
     # a batch whose single split does not fit
@@ -127,3 +143,29 @@ def test_sizes_beyond_the_limit_are_refused():
     a.q_stride[0] = a.o_stride[0] = 0
     a.k_stride[0] = a.v_stride[0] = 0
     assert lib.af_decode_noalloc(a, stream) == N.AF_ERR_WORKSPACE
+
+
+def test_graph_capture_after_the_first_call():
+    """After an eager call on the GPU, a captured af_decode_noalloc replays
+    bit for bit like af_decode, with eager work between replays (the inputs
+    are rewritten and the output cleared before each replay)."""
+    B, Hq, Hkv, N_kv, D = 2, 16, 4, 3000, 128
+    print(f"[noalloc] graph capture B={B} Hq={Hq} N={N_kv}", flush=True)
+    lib = N.lib()
+    Q, K, V = _make(B, Hq, Hkv, N_kv, D, torch.bfloat16, 7)
+    S = _default_splits(B, Hq, Hkv, N_kv, D)
+    o_first, _ = _both(Q, K, V, S)           # the first call, eager
+    o_g = torch.full_like(Q, float("nan"))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        N.check(lib.af_decode_noalloc(_args(Q, K, V, o_g), torch.cuda.current_stream().cuda_stream))
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    for rep in range(3):
+        Q.copy_(torch.randn(Q.shape, generator=gen, device="cuda", dtype=Q.dtype))
+        o_g.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        _, o_ref = _both(Q, K, V, S)
+        assert torch.equal(o_g, o_ref), rep
+    want = O.naive_attention(Q.cpu(), K.cpu(), V.cpu())
+    assert (o_g.float().cpu() - want).abs().max().item() <= TOL[torch.bfloat16]
