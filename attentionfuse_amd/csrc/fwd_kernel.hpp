@@ -108,6 +108,9 @@ template <int D, int MASK, int BIAS, int NORM>
 constexpr int fwd_waves_per_eu() {
   if (D > 64) return 1;
   if (fwd_defer<D, MASK, BIAS, NORM>()) return 2;
+  // an additive bias tile takes 8 loaded values per score block: at three
+  // waves these kernels spilled 18-36 registers, with ReLU about 300
+  if (BIAS == BIAS_ADD) return 2;
   return (BIAS == BIAS_ALIBI && MASK != MASK_SW && MASK != MASK_BS && MASK != MASK_BSE) ? 2 : 3;
 }
 
@@ -717,6 +720,10 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     constexpr bool PV = decltype(pv_on)::value;
     constexpr int M = PV ? kSM + kPM : kSM;
     constexpr int A = M < kOpAhead ? M : kOpAhead;
+    // pairs whose softmax starts in one chunk, and chunks between starts
+    constexpr int PPC = kPairs >= M ? kPairs / M : 1;
+    constexpr int CPP = M >= kPairs ? M / kPairs : 1;
+    static_assert(PPC * M == kPairs * CPP, "pairs spread evenly over the chunks");
     // MFMA i: with PV even i is score MFMA i/2 and odd i P V MFMA i/2
     auto read_op = [&](int i) -> u32x4 {
       if (PV && (i & 1)) return read_vop(vpar, i >> 1);
@@ -740,21 +747,28 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
         }
       }
       if (c + A < M) op[c + A] = read_op(c + A);
+      // stage st of pair p runs in chunk p * M / kPairs + st: PPC pairs
+      // start in every CPP-th chunk
 #pragma unroll
-      for (int p = 0; p < kPairs; ++p) {
-        const int cp = p * M / kPairs;      // chunk of the pair's first stage
-        const int kb = p >> 3, r = 2 * (p & 7);
-        if (c == cp) {
-          s[kb][r] = __builtin_fmaf(s[kb][r], lg.zc, lg.off[kb]);
-          s[kb][r + 1] = __builtin_fmaf(s[kb][r + 1], lg.zc, lg.off[kb]);
-        } else if (c == cp + 1) {
-          s[kb][r] = __builtin_amdgcn_exp2f(s[kb][r]);
-          s[kb][r + 1] = __builtin_amdgcn_exp2f(s[kb][r + 1]);
-        } else if (c == cp + 2) {
-          const uint32_t w2 = E::pack(s[kb][r], s[kb][r + 1]);
-          pf[2 * kb + (r >> 3)][(r & 7) >> 1] = w2;
-          if (p < 4) E::dot_first(w2, ts[p & 3]);
-          else E::dot_pair(w2, ts[p & 3]);
+      for (int st = 0; st < 3; ++st) {
+        const int cs = c - st;
+        if (cs < 0 || cs % CPP != 0 || cs / CPP * PPC >= kPairs) continue;
+#pragma unroll
+        for (int jp = 0; jp < PPC; ++jp) {
+          const int p = cs / CPP * PPC + jp;
+          const int kb = p >> 3, r = 2 * (p & 7);
+          if (st == 0) {
+            s[kb][r] = __builtin_fmaf(s[kb][r], lg.zc, lg.off[kb]);
+            s[kb][r + 1] = __builtin_fmaf(s[kb][r + 1], lg.zc, lg.off[kb]);
+          } else if (st == 1) {
+            s[kb][r] = __builtin_amdgcn_exp2f(s[kb][r]);
+            s[kb][r + 1] = __builtin_amdgcn_exp2f(s[kb][r + 1]);
+          } else {
+            const uint32_t w2 = E::pack(s[kb][r], s[kb][r + 1]);
+            pf[2 * kb + (r >> 3)][(r & 7) >> 1] = w2;
+            if (p < 4) E::dot_first(w2, ts[p & 3]);
+            else E::dot_pair(w2, ts[p & 3]);
+          }
         }
       }
       __builtin_amdgcn_sched_barrier(0);
