@@ -540,9 +540,16 @@ struct BsTiles {
     const int e = t / sub;
     return bs_row_get(a, na, b, e0 + e) * blk + (t - e * sub) * tile + (part_of(e0 + e) ? 1 : 0);
   }
-  // lanes past the walk's last tile hold 0 and read no list entry
+  // Lanes past the walk's last tile hold 0.  A lane's entry of list a (and
+  // its partial flag) is loaded before the list count is known, inside the
+  // padded row of `wa` entries: the count, read from memory in parallel,
+  // then only selects.  Loaded after it instead, the entries added one
+  // memory round trip to the start of every block-sparse workgroup (2500
+  // cycles of the measured 6000 before a forward workgroup's first tile).
+  // List b, which entries at or past the count come from, is read only by
+  // the lanes that need it.
   __device__ void init(const int32_t* a_, int na_, const int32_t* b_, int e0_, int sub_, int blk_, int tile_,
-                       int ntiles, int lane, int pmode_ = 0, const int32_t* flags_ = nullptr) {
+                       int ntiles, int lane, int64_t wa, int pmode_ = 0, const int32_t* flags_ = nullptr) {
     a = a_;
     na = na_;
     b = b_;
@@ -552,12 +559,19 @@ struct BsTiles {
     tile = tile_;
     pmode = pmode_;
     flags = flags_;
-    auto at = [&](int t) -> int {
-      if (t >= ntiles) return 0;
-      const int e = e0 + t / sub;
-      return (e < na ? a[e] : b[e - na]) * blk + (t % sub) * tile + (part_of(e) ? 1 : 0);
-    };
-    lo = at(lane);
+    const int e = e0 + lane / sub;
+    // The entry index clamped into the row (wa >= 1, checked on the host):
+    // every lane loads unconditionally.  A condition around the load made the
+    // compiler emit an invalid aperture check in some instantiations.
+    const int ec = (int)min<int64_t>(e, wa - 1);
+    const int va = a[ec];
+    const int fl = pmode == 2 ? flags[ec] : 0;
+    if (lane >= ntiles) {
+      lo = 0;
+    } else {
+      const bool part = pmode == 1 ? e >= na : fl != 0;
+      lo = (e < na ? va : b[e - na]) * blk + (lane % sub) * tile + (part ? 1 : 0);
+    }
   }
   __device__ __forceinline__ int raw(int t) const {
     if (t < 64) return __builtin_amdgcn_readlane(lo, t);

@@ -446,6 +446,8 @@ int af_fwd_blocksparse(const af_fwd_args* a, const af_blockmask* bm, void* works
   if (bm == nullptr || bm->full_kv_num == nullptr || bm->full_kv_idx == nullptr ||
       bm->kv_num_blocks == nullptr || bm->kv_indices == nullptr)
     return fail(AF_ERR_BAD_ARG, "block mask lists are NULL");
+  if (bm->full_kv_stride < 1 || bm->kv_stride < 1)
+    return fail(AF_ERR_BAD_ARG, "block mask row strides must be at least 1");
   if (bm->block_m != 32 && bm->block_m != 64 && bm->block_m != 128)
     return fail(AF_ERR_UNSUPPORTED, "block-sparse BLOCK_M=%d: supported 32, 64, 128", bm->block_m);
   // key blocks are walked in 64-key stages (fp32: 32-key tiles)

@@ -146,6 +146,8 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
     if (bm == nullptr || bm->full_kv_num == nullptr || bm->full_kv_idx == nullptr || bm->kv_num_blocks == nullptr ||
         bm->kv_indices == nullptr || bm->q_num_blocks == nullptr || bm->q_indices == nullptr)
       return bad(AF_ERR_BAD_ARG, "block-sparse backward needs the Q-major and K-major block lists");
+    if (bm->full_kv_stride < 1 || bm->kv_stride < 1 || bm->q_stride < 1)
+      return bad(AF_ERR_BAD_ARG, "block mask row strides must be at least 1");
     if ((bm->block_m != 64 && bm->block_m != 128) || (bm->block_n != 64 && bm->block_n != 128))
       return bad(AF_ERR_UNSUPPORTED, "block-sparse backward supports 64 or 128 blocks");
     if (bm->n_q_blocks != (a->seqlen_q + bm->block_m - 1) / bm->block_m ||

@@ -469,7 +469,7 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
   }
   BsTiles bst;
   if constexpr (kIsBs<MASK>)
-    bst.init(bs_row, bs_n, bs_row, bs_e0, bs_sub, p.bs_block_m, 32, ntq, lane,
+    bst.init(bs_row, bs_n, bs_row, bs_e0, bs_sub, p.bs_block_m, 32, ntq, lane, p.bs_q_rs,
              MASK == MASK_BSE ? 2 : 0,
              p.bs_q_partial != nullptr ? p.bs_q_partial + kb * p.bs_q_rs : nullptr);
   auto tile_m0 = [&](int t) -> int {
@@ -838,7 +838,7 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
   }
   BsTiles bst;
   if constexpr (kIsBs<MASK>)
-    bst.init(bs_full_row, bs_nfull, bs_part_row, bs_e0, bs_sub, p.bs_block_n, 32, ntiles, lane,
+    bst.init(bs_full_row, bs_nfull, bs_part_row, bs_e0, bs_sub, p.bs_block_n, 32, ntiles, lane, p.bs_full_rs,
              MASK == MASK_BSE ? 1 : 0);
   auto tile_n0 = [&](int t) -> int {
     if constexpr (kIsBs<MASK>) {

@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   }
   BsTiles bst;
   if constexpr (kIsBs<MASK>)
-    bst.init(bs_full_row, bs_nfull, bs_part_row, bs_e0, bs_sub, p.bs_block_n, BN, ntiles, lane,
+    bst.init(bs_full_row, bs_nfull, bs_part_row, bs_e0, bs_sub, p.bs_block_n, BN, ntiles, lane, p.bs_full_rs,
              MASK == MASK_BSE ? 1 : 0);
   // Causal-type ALiBi walks the key tiles from the diagonal down: its bias
   // -slope (i - j) then only falls from tile to tile, so the running max set

@@ -85,7 +85,7 @@ typedef struct af_blockmask {
   const int32_t* kv_indices;    /* (n_q_blocks, kv_stride)      */
   const int32_t* q_num_blocks;  /* (n_kv_blocks)                */
   const int32_t* q_indices;     /* (n_kv_blocks, q_stride)      */
-  int64_t full_kv_stride, kv_stride, q_stride;
+  int64_t full_kv_stride, kv_stride, q_stride;  /* row strides = padded row widths, >= 1 */
   int32_t block_m, block_n, n_q_blocks, n_kv_blocks;
   /* Optional work plans written by af_blockmask_plan, device int32 (all
    * NULL / 0: one workgroup per query block and per key block, the
