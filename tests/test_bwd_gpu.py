@@ -104,6 +104,17 @@ def test_backward_head_dims(name, D):
     check(run(name, 1, 4, 4, 192, D, torch.bfloat16), torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("name,N", [("dense", 333), ("causal", 700), ("sw", 600), ("sw_causal", 520),
+                                    ("rope_causal", 777), ("rope_dense", 256)])
+def test_backward_d128_masks_ragged(name, N, dtype):
+    """Head dim 128 with GQA 4:1 at ragged lengths, every dense mask: key
+    blocks that end past N_kv, waves with no keys, a 48-key window narrower
+    than a workgroup's key block."""
+    print(f"[bwd] D=128 {name} N={N} {dtype}", flush=True)
+    check(run(name, 1, 8, 2, N, 128, dtype), dtype)
+
+
 @pytest.mark.parametrize("heads", [(8, 2), (8, 1), (12, 4), (32, 8)])
 @pytest.mark.parametrize("name", ["causal", "rope_causal"])
 def test_backward_gqa_group_sum(name, heads):
