@@ -501,6 +501,28 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // ---------------------------------------------------------------------------
+// Work item and (batch, head) of workgroup g of a grid of n_items x BH
+// workgroups.  The dispatcher hands workgroup g to XCD g % 8, so with BH a
+// multiple of 8 the default order (item-major, head-minor) keeps every head
+// on one XCD, but an XCD then walks all BH / 8 of its heads at once.  With
+// gh > 0 (BH a multiple of 8 gh) it walks them gh at a time, every item of
+// a group before the next group, so that the rows a group's workgroups
+// re-read (block-sparse walks load each listed tile once per list that
+// names it) stay in the XCD's L2.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void xcd_head_groups(int g, int BH, int n_items, int gh, int& item, int& bh) {
+  if (gh <= 0) {
+    bh = g % BH;
+    item = g / BH;
+    return;
+  }
+  const int x = g & 7, k = g >> 3, per = gh * n_items;
+  const int grp = k / per, r = k - grp * per;
+  item = r / gh;
+  bh = x + 8 * (grp * gh + (r - item * gh));
+}
+
+// ---------------------------------------------------------------------------
 // Entry e (wave-uniform) of one BlockMask row: list a, then list b.  The
 // lists are read through the constant address space, so the compiler loads
 // them with scalar loads (s_load_dword, counted by lgkmcnt).  Through a

@@ -493,6 +493,9 @@ int af_fwd_blocksparse(const af_fwd_args* a, const af_blockmask* bm, void* works
       p.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.part_ml);
     }
   }
+  // each listed key tile is re-read by every row that lists it: K and V of
+  // a head
+  p.bs_xcd_heads = bs_xcd_heads(a->batch * a->heads_q, 2 * (int64_t)a->seqlen_kv * a->key.head_dim * 2);
   if ((rc = dispatch_fwd(p, *a, bm->block_m / 32, workspace, workspace_bytes, s))) return rc;
   if (!split) return AF_OK;
   BsFwdCombineParams c;

@@ -302,6 +302,14 @@ int run_bwd(const af_bwd_args* a, const af_blockmask* bm, void* workspace, size_
   p.split_keys = std::min(p.n_split_kb * BK, a->seqlen_kv);
   g.dkv = (unsigned)std::max(1, (p.n_split_kb * p.g_split + (kv_rows - p.n_split_kb)) * a->batch * a->heads_kv);
   g.dq = (unsigned)std::max(1, q_rows * a->batch * a->heads_q);
+  if (k.mask == AF_MASK_BLOCK_SPARSE) {
+    // the dQ walk re-reads k~ and V of its head, the dK/dV walk q~ and dO
+    // of the G query heads of its key/value head
+    const int64_t row_bytes = (int64_t)k.head_dim * 2;
+    p.bs_q_rows = q_rows;
+    p.bs_xcd_heads_q = bs_xcd_heads(a->batch * a->heads_q, 2 * a->seqlen_kv * row_bytes);
+    p.bs_xcd_heads_kv = bs_xcd_heads(a->batch * a->heads_kv, 2 * (int64_t)p.G * a->seqlen_q * row_bytes);
+  }
   g.combine = 0;
   if (p.g_split > 1) {
     const int64_t krows = (int64_t)a->batch * a->heads_kv * p.split_keys;

@@ -137,6 +137,10 @@ struct BwdParams {
   float* part_dv;
   // bwd_dkvdq_kernel: workgroups [0, n_dkv_wg) run dK/dV, the rest dQ
   int32_t n_dkv_wg;
+  // block-sparse walks: rows of the dQ grid (plan items or query blocks),
+  // and heads per XCD group of the dQ and the dK/dV grids
+  // (xcd_head_groups), 0 = off
+  int32_t bs_q_rows, bs_xcd_heads_q, bs_xcd_heads_kv;
   float scale;
 };
 
@@ -396,7 +400,10 @@ __device__ __forceinline__ void bwd_dkv_body(const BwdParams& p, uint16_t* lds, 
   // split key blocks first (g_split workgroups each), then unsplit ones
   const int heavy_wg = p.n_split_kb * BHK * p.g_split;
   int kbi, rem, gsplit = p.g_split;
-  if (wg < heavy_wg) {
+  if (kIsBs<MASK> && p.g_split == 1 && p.bs_xcd_heads_kv > 0) {
+    // every key-block row unsplit: grid n_split_kb x BHK
+    xcd_head_groups(wg, BHK, p.n_split_kb, p.bs_xcd_heads_kv, kbi, rem);
+  } else if (wg < heavy_wg) {
     kbi = wg / (BHK * p.g_split);
     rem = wg - kbi * (BHK * p.g_split);
   } else {
@@ -785,8 +792,9 @@ __device__ __forceinline__ void bwd_dq_body(const BwdParams& p, uint16_t* lds, i
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int BH = p.B * p.Hq;
-  const int bh = wg % BH;
-  const int mbi = wg / BH;
+  int bh = wg % BH;
+  int mbi = wg / BH;
+  if constexpr (kIsBs<MASK>) xcd_head_groups(wg, BH, p.bs_q_rows, p.bs_xcd_heads_q, mbi, bh);
   const bool heavy_last = MASK == MASK_CAUSAL || MASK == MASK_CSW;
   // block-sparse plan item: a piece [e0, e0 + ne) of row mb's list
   int mb = heavy_last ? (p.n_qblocks - 1 - mbi) : mbi;

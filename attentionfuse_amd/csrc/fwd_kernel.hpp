@@ -76,6 +76,8 @@ struct FwdParams {
   int64_t bs_full_rs, bs_part_rs;
   int32_t B, Hq, Hkv, Nq, Nkv, G;
   int32_t n_mblocks, bs_block_m, bs_block_n;
+  // block-sparse walks: heads per XCD group (xcd_head_groups), 0 = off
+  int32_t bs_xcd_heads;
   int32_t cov_nq, cov_nk;
   int32_t rope_len;
   float scale;
@@ -142,8 +144,9 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // m-block-major order: the heaviest query blocks of every head first.
   // Workgroup g runs on XCD g % 8, so when B*H is a multiple of 8 each XCD
   // works on a fixed eighth of the heads, whose K/V stay in its L2.
-  const int bh = blockIdx.x % BH;
-  const int mbi = blockIdx.x / BH;
+  int bh = blockIdx.x % BH;
+  int mbi = blockIdx.x / BH;
+  if constexpr (kIsBs<MASK>) xcd_head_groups(blockIdx.x, BH, p.n_mblocks, p.bs_xcd_heads, mbi, bh);
   const bool heavy_last = MASK == MASK_CAUSAL || MASK == MASK_CSW;
   // block-sparse plan item: a piece [e0, e0 + ne) of row mb's list
   int mb = heavy_last ? (p.n_mblocks - 1 - mbi) : mbi;

@@ -46,6 +46,23 @@ AF_DECLARE_ROPE(launch_rope_bf16_d128)
 AF_DECLARE_ROPE(launch_rope_bf16_d256)
 #undef AF_DECLARE_ROPE
 
+// Heads per XCD group of a block-sparse grid over BH heads
+// (xcd_head_groups): the largest divisor of BH / 8 whose heads' re-read rows
+// (head_bytes each) fit AF_BS_L2_BUDGET bytes, at least 1; 0 (the default
+// order) when BH is not a multiple of 8.  An XCD's L2 is 4 MiB and also
+// holds the rows read once and the outputs.
+#ifndef AF_BS_L2_BUDGET
+#define AF_BS_L2_BUDGET (3 << 20)
+#endif
+inline int bs_xcd_heads(int BH, int64_t head_bytes) {
+  if (AF_BS_L2_BUDGET <= 0 || BH <= 0 || BH % 8 != 0) return 0;
+  const int per = BH / 8;
+  int gh = 1;
+  for (int d = 1; d <= per; ++d)
+    if (per % d == 0 && (int64_t)d * head_bytes <= (int64_t)AF_BS_L2_BUDGET) gh = d;
+  return gh;
+}
+
 // fp32 forward and fp32 key rotation, defined in fwd_f32.hip; return -1 for
 // a head dim with no instantiation.
 struct FwdF32Params;
