@@ -364,6 +364,17 @@ __device__ __forceinline__ int tr_at(int lane, int t, int db) {
   return lds_at<D>(row, col);
 }
 
+// Byte offset of element col of row `row` (16-bit elements, rows `stride`
+// elements apart) in 32-bit arithmetic: buffer offsets stay below the 4 GiB
+// range (checked on the host).  The empty asm keeps the multiply and the add
+// apart: fused, they became a 64-bit multiply-add whose register pair the
+// register allocator kept (and spilled) for the whole kernel.
+__device__ __forceinline__ uint32_t dma_off(int row, int64_t stride, int col) {
+  uint32_t prod = (uint32_t)row * (uint32_t)stride;
+  asm("" : "+v"(prod));
+  return (prod + (uint32_t)col) * 2u;
+}
+
 // Staging of two row tiles (rows [r0, r0 + ROWS) of tensors A and B, D
 // elements each) straight from global memory into one swizzled LDS stage --
 // tile A at element 0 of the stage, tile B at element ROWS * D -- with
@@ -404,7 +415,7 @@ struct TileDma {
     const bool isb = pos >= CHUNKS;
     const int rem = isb ? pos - CHUNKS : pos;
     const int row = rem / (D / 8), kp = rem % (D / 8);
-    return (uint32_t)((row * (isb ? bstride : astride) + 8 * (kp ^ lds_swz<D>(row))) * 2);
+    return dma_off(row, isb ? bstride : astride, 8 * (kp ^ lds_swz<D>(row)));
   }
   __device__ void init(int w, int lane, int64_t astride, int64_t bstride) {
     if constexpr (SHARED) {
@@ -451,7 +462,7 @@ struct RowsDma {
   __device__ static uint32_t lane_off(int m, int lane, int64_t stride) {
     const int pos = 64 * m + lane;
     const int row = pos / (D / 8), kp = pos % (D / 8);
-    return (uint32_t)((row * stride + 8 * (kp ^ lds_swz<D>(row))) * 2);
+    return dma_off(row, stride, 8 * (kp ^ lds_swz<D>(row)));
   }
   __device__ void init(int w, int lane, int64_t stride) {
     if constexpr (SHARED) {

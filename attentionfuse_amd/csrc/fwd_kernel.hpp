@@ -899,40 +899,46 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // this lane's 32 keys of every tile, plus the partner lane's 32
   float lt = lsum[0] + lsum[1];
   lt += xor32(lt);
+  // The lane's row and half are taken from the lane id again: kept from
+  // the prologue, the compiler spilled them (and a 64-bit copy of the row)
+  // across the loop at three waves per SIMD.
+  int le = __lane_id();
+  asm volatile("" : "+v"(le));
+  const int he = le >> 5, qre = q0w + (le & 31);
   if (kIsBs<MASK> && bs_slot >= 0) {
     // a piece of a split row: unnormalised O and (m, l) for the combine
-    if (qrow < p.Nq) {
-      const int64_t prow = ((int64_t)bs_slot * BH + bh) * BM + (qrow - m0);
+    if (qre < p.Nq) {
+      const int64_t prow = ((int64_t)bs_slot * BH + bh) * BM + (qre - m0);
       float* orow = p.part_o + prow * D;
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<f32x4*>(orow + 32 * db + 8 * g + 4 * h) =
+          *reinterpret_cast<f32x4*>(orow + 32 * db + 8 * g + 4 * he) =
               f32x4{o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
-      if (h == 0) *reinterpret_cast<f32x2*>(p.part_ml + 2 * prow) = f32x2{m_run, lt};
+      if (he == 0) *reinterpret_cast<f32x2*>(p.part_ml + 2 * prow) = f32x2{m_run, lt};
     }
     return;
   }
   const float inv = (lt == 0.f) ? 1.f : 1.f / lt;
-  if (qrow < p.Nq) {
-    uint16_t* orow = p.o + b * p.os[0] + hq * p.os[1] + (int64_t)qrow * p.os[2];
+  if (qre < p.Nq) {
+    uint16_t* orow = p.o + b * p.os[0] + hq * p.os[1] + (int64_t)qre * p.os[2];
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int d0 = 32 * db + 8 * g + 4 * h;
+        const int d0 = 32 * db + 8 * g + 4 * he;
         u32x2 w2;
         w2[0] = E::pack(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
         w2[1] = E::pack(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
         *reinterpret_cast<u32x2*>(orow + d0) = w2;
       }
-    if (p.lse != nullptr && h == 0) {
+    if (p.lse != nullptr && he == 0) {
       float L = -INFINITY;
       if constexpr (NORM == NORM_SOFTMAX) {
         if (lt > 0.f) L = (m_run + __log2f(lt)) * kLn2;
       }
-      p.lse[b * p.ls[0] + hq * p.ls[1] + (int64_t)qrow * p.ls[2]] = L;
+      p.lse[b * p.ls[0] + hq * p.ls[1] + (int64_t)qre * p.ls[2]] = L;
     }
   }
 }
