@@ -116,8 +116,8 @@ constexpr int fwd_waves_per_eu() {
   return (BIAS == BIAS_ALIBI && MASK != MASK_SW && MASK != MASK_BS && MASK != MASK_BSE) ? 2 : 3;
 }
 
-// Head dims up to 64 fit in 168 VGPRs (a few setup values spill outside the
-// loop): three waves per SIMD, three 4-wave workgroups per CU.
+// Head dims up to 64 fit in 168 VGPRs: three waves per SIMD, three 4-wave
+// workgroups per CU.
 template <class E, int D, int MASK, int BIAS, int NORM, bool ROPE, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(fwd_waves_per_eu<D, MASK, BIAS, NORM>())))
     fwd_kernel(const FwdParams p) {
