@@ -211,3 +211,37 @@ def test_lists_edited_in_place_between_launches():
         assert (out.double().cpu() - o_ref).abs().max().item() <= TOL[torch.float16]
         for got, ref in ((dq, rq), (dk, rk), (dv, rv)):
             assert ((got.double().cpu() - ref).norm() / ref.norm()).item() <= GRAD_REL
+
+
+def test_one_head_per_xcd_group():
+    """Sixteen heads of dimension 128 at length 4096 under the BigBird
+    fixture mask: one head's K/V (2 MiB) fills an XCD's share of L2, so the
+    forward, dQ and dK/dV grids all walk the heads one per XCD at a time
+    (two groups of eight).  Every (head, tile) must be visited once (forward
+    coverage counters) and every head must match the oracle."""
+    from attnfuse.runtime.block_mask import run_block_sparse_backward
+    print("[bs] one head per XCD group, 2x8 heads D=128 N=4096", flush=True)
+    fx = json.loads((Path(__file__).parent / "golden" / "bigbird_c4_grid.json").read_text())
+    n = fx["n_blocks"]
+    grid = torch.zeros(n, n, dtype=torch.bool)
+    for a, row in enumerate(fx["rows"]):
+        grid[a, row] = True
+    Nn, Dn, Bn, Hn = 64 * n, 128, 2, 8
+    bm = block_mask_from_blocks(grid, 64, 64, device="cuda")
+    Q, K, V, dO = make(Bn, Hn, Nn, Dn, torch.float16, seed=6)
+    cov = torch.zeros(Bn, Hn, Nn // 32, Nn // 64, dtype=torch.int32, device="cuda")
+    lse = torch.empty(Q.shape[:3], device="cuda", dtype=torch.float32)
+    out = run_block_sparse(Q, K, V, bm, Dn ** -0.5, save_lse=lse, coverage=cov)
+    dq, dk, dv = run_block_sparse_backward(Q, K, V, out, lse, dO, bm, Dn ** -0.5)
+    torch.cuda.synchronize()
+    exp_cov = O.expected_coverage(Nn, Nn, mask="block_sparse", grid=grid, bm=64, bn=64)
+    assert torch.equal(cov.cpu(), exp_cov.expand(Bn, Hn, *exp_cov.shape))
+    em = elem_mask(grid, Nn)
+    for b in range(Bn):
+        for h in range(Hn):
+            sl = (slice(b, b + 1), slice(h, h + 1))
+            o_ref, rq, rk, rv = O.attention_grads(Q[sl].cpu(), K[sl].cpu(), V[sl].cpu(), dO[sl].cpu(),
+                                                  dtype=torch.float32, elem_mask=em)
+            assert (out[sl].float().cpu() - o_ref).abs().max().item() <= TOL[torch.float16], (b, h)
+            for got, ref in ((dq[sl], rq), (dk[sl], rk), (dv[sl], rv)):
+                assert ((got.float().cpu() - ref).norm() / ref.norm()).item() <= GRAD_REL, (b, h)
