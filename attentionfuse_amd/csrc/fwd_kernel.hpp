@@ -101,13 +101,28 @@ constexpr bool fwd_defer() {
   return BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW || MASK == MASK_FULL);
 }
 
-// Waves per SIMD the register budget is set for: head dims up to 64 fit
-// 168 VGPRs (three waves), except ALiBi: the causal-type kind's initial
-// score accumulator takes 16 more, and the dense kind's lazy steps spilled
-// 300 registers' worth at three waves (two waves); D = 128 takes one.  The
-// deferred pipeline keeps two score tiles and two P tiles live (two waves).
+// Whether a forward instantiation runs the unpipelined step (see the
+// kernel): softmax without a bias over a dense, causal or windowed walk at
+// head dims up to 64.  It holds one score tile instead of two (112-115
+// VGPRs), so four waves run per SIMD.  Same-box A/B against the pipelined
+// step at three waves, outputs bit-identical: config 2 1.5-2 %, the dense
+// and windowed forwards 3.5-6 % faster.  At head dim 128 it saved too few
+// registers for a third wave (186 VGPRs) and was 1-2 % slower.
+template <int D, int MASK, int BIAS, int NORM>
+constexpr bool fwd_unpipelined() {
+  return D <= 64 && BIAS == BIAS_NONE && NORM == NORM_SOFTMAX &&
+         (MASK == MASK_FULL || MASK == MASK_CAUSAL || MASK == MASK_SW || MASK == MASK_CSW);
+}
+
+// Waves per SIMD the register budget is set for: the unpipelined step four;
+// other head dims up to 64 fit 168 VGPRs (three waves), except ALiBi: the
+// causal-type kind's initial score accumulator takes 16 more, and the dense
+// kind's lazy steps spilled 300 registers' worth at three waves (two
+// waves); D = 128 takes one.  The deferred pipeline keeps two score tiles
+// and two P tiles live (two waves).
 template <int D, int MASK, int BIAS, int NORM>
 constexpr int fwd_waves_per_eu() {
+  if (fwd_unpipelined<D, MASK, BIAS, NORM>()) return 4;
   if (D > 64) return 1;
   if (fwd_defer<D, MASK, BIAS, NORM>()) return 2;
   // an additive bias tile takes 8 loaded values per score block: at three
@@ -116,8 +131,8 @@ constexpr int fwd_waves_per_eu() {
   return (BIAS == BIAS_ALIBI && MASK != MASK_SW && MASK != MASK_BS && MASK != MASK_BSE) ? 2 : 3;
 }
 
-// Head dims up to 64 fit in 168 VGPRs: three waves per SIMD, three 4-wave
-// workgroups per CU.
+// Head dims up to 64 run three or four waves per SIMD (three or four 4-wave
+// workgroups per CU, 32 KB of LDS each).
 template <class E, int D, int MASK, int BIAS, int NORM, bool ROPE, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(fwd_waves_per_eu<D, MASK, BIAS, NORM>())))
     fwd_kernel(const FwdParams p) {
@@ -789,16 +804,18 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   // last read by the score MFMAs of iteration t-1; V(t+1) overwrites V(t-1),
   // last read in iteration t-1; the barrier closing each iteration separates
   // the two.
-  // The deferred pipeline (below) loads V(t) in step t instead.
+  // The deferred pipeline (below) loads V(t) in step t instead, and the
+  // unpipelined step loads K(t+1) and V(t+1).
+  constexpr bool kUnpiped = fwd_unpipelined<D, MASK, BIAS, NORM>();
   if (ntiles > 0) {
     load_k(0, 0);
     if constexpr (!kDefer) load_v(0, 0);
   }
-  if (ntiles > 1) load_k(1, 1);
+  if (!kUnpiped && ntiles > 1) load_k(1, 1);
   wait_lds_dma();
   __syncthreads();
   f32x16 sa[BN / 32], sb[BN / 32];
-  if (ntiles > 0) scores(0, sa);
+  if (!kUnpiped && ntiles > 0) scores(0, sa);
   // Step 0 loads K(2) into slot 0, which every wave has just read for
   // scores(0): no wave may issue that load before all of them have their
   // K(0) operands (each wave's reads complete before it reaches the
@@ -866,6 +883,52 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
       // P(ntiles-1) is in pa for an even tile index, pb for an odd one
       if ((ntiles - 1) & 1) pv_pipe(1, pb);
       else pv_pipe(0, pa);
+    }
+  } else if constexpr (kUnpiped) {
+    // Step t computes the scores, P and P V of tile t from slots t & 1 and
+    // loads K(t+1), V(t+1) into the other slots, which every wave left at
+    // the barrier closing step t-1.  The loads are issued after the score
+    // MFMAs (issued first they delayed them: 1-2 % slower).  A lazy step
+    // that fails its test recomputes the scores from the K slot, which
+    // still holds K(t).  One score tile live instead of two leaves room for
+    // four waves per SIMD, whose interleaving covers what the pipelined
+    // step overlapped inside one wave.
+    auto step_unpiped = [&](int t, int par, bool exact) {
+      u32x4 kop[KS];
+      read_k(par, kop);
+      __builtin_amdgcn_sched_barrier(0);
+      scores_k(par, kop, sa);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 1 < ntiles) {
+        load_k(t + 1, par ^ 1);
+        load_v(t + 1, par ^ 1);
+      }
+      u32x4 pf[BN / 16];
+      if (exact) {
+        const Logit lg = rebase(sa, bias_mask(t, sa, true));
+        softmax_tile(sa, lg, pf);
+        add_rowsum(pf);
+      } else {
+        Logit lg = bias_mask(t, sa, true);
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb) lg.off[kb] -= m_run;
+        softmax_tile(sa, lg, pf);
+        float tsum = tile_rowsum(pf);
+        if (__builtin_amdgcn_ballot_w64(!(tsum < kRedo)) != 0) {
+          scores(par, sa);
+          const Logit lg1 = rebase(sa, bias_mask(t, sa, false));
+          softmax_tile(sa, lg1, pf);
+          tsum = tile_rowsum(pf);
+        }
+        lsum[0] += tsum;
+      }
+      pv_pipe(par, pf);
+      close();
+    };
+    if (ntiles > 0) step_unpiped(0, 0, true);
+    for (int t = 1; t < ntiles; t += 2) {
+      step_unpiped(t, 1, false);
+      if (t + 1 < ntiles) step_unpiped(t + 1, 0, false);
     }
   } else if constexpr (kLazy) {
     if (ntiles > 0) {
