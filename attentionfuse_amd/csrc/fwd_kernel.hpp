@@ -27,7 +27,11 @@
 //    exceeds it by more than 2^kTau, so the O rescale is rare.
 //  * Q stays in registers for the whole kernel, rotated once.
 //  * causal grids run the longest query blocks first.
-//  * ALiBi and block-sparse kernels defer P V by one step (fwd_defer): the
+//  * softmax kernels with no bias or ALiBi at head dims up to 64 run each
+//    tile's scores, P and P V in one unpipelined step (fwd_unpipelined), and
+//    the registers that saves buy a fourth (ALiBi: third) wave per SIMD;
+//    other kernels compute the scores of tile t+1 while P of tile t is on
+//    the VALU.  Block-sparse kernels defer P V by one step (fwd_defer): the
 //    score MFMAs of tile t+1 and the P V MFMAs of tile t-1 alternate, one
 //    per chunk, with the softmax VALU work of tile t in one basic block.
 #pragma once
@@ -84,45 +88,44 @@ struct FwdParams {
   int32_t window;
 };
 
+// Whether a forward instantiation runs the unpipelined step (see the
+// kernel): softmax with no bias or ALiBi over a dense, causal or windowed
+// walk at head dims up to 64.  It holds one score tile instead of two, so
+// the kernels without a bias hold 112-115 VGPRs and run four waves per SIMD,
+// the ALiBi kernels (whose initial score accumulator takes 16 more) 125-168
+// and three or four.  Same-box A/B against the pipelined steps: config 2
+// 1.5-2 %, the dense and windowed forwards 3.5-6 % faster (three waves
+// before, outputs bit-identical); config 2 with ALiBi 7 %, dense ALiBi 10 %
+// and windowed ALiBi 3 % faster (the first two against the deferred P V
+// pipeline at two waves).  At head dim 128 the step saved too few
+// registers for a third wave (186 VGPRs) and was 1-2 % slower.
+template <int D, int MASK, int BIAS, int NORM>
+constexpr bool fwd_unpipelined() {
+  return D <= 64 && (BIAS == BIAS_NONE || BIAS == BIAS_ALIBI) && NORM == NORM_SOFTMAX &&
+         (MASK == MASK_FULL || MASK == MASK_CAUSAL || MASK == MASK_SW || MASK == MASK_CSW);
+}
+
 // Whether a forward instantiation runs the deferred P V pipeline (see the
-// kernel): lazy softmax kernels with head dims up to 64 that already run two
-// waves per SIMD (ALiBi) or walk a block mask.  Measured on MI355X (same-box
-// A/B, config 2's shape): ALiBi 1-2 % and the BigBird forward 2-3 % faster;
-// the causal kernel without a bias, which otherwise runs three waves per
-// SIMD, 3-4 % slower at the deferred pipeline's two.
+// kernel): the block-sparse softmax walks without ALiBi at head dims up to
+// 64 (two waves per SIMD; the BigBird forward 2-3 % faster than the
+// pipelined step).
 #ifndef AF_FWD_DEFER
 #define AF_FWD_DEFER 1
 #endif
 template <int D, int MASK, int BIAS, int NORM>
 constexpr bool fwd_defer() {
   if (!AF_FWD_DEFER || D > 64 || NORM != NORM_SOFTMAX) return false;
-  if (MASK == MASK_BS || MASK == MASK_BSE) return BIAS != BIAS_ALIBI;
-  // ALiBi is lazy where its walk makes the bias fall from tile to tile
-  return BIAS == BIAS_ALIBI && (MASK == MASK_CAUSAL || MASK == MASK_CSW || MASK == MASK_FULL);
+  return (MASK == MASK_BS || MASK == MASK_BSE) && BIAS != BIAS_ALIBI;
 }
 
-// Whether a forward instantiation runs the unpipelined step (see the
-// kernel): softmax without a bias over a dense, causal or windowed walk at
-// head dims up to 64.  It holds one score tile instead of two (112-115
-// VGPRs), so four waves run per SIMD.  Same-box A/B against the pipelined
-// step at three waves, outputs bit-identical: config 2 1.5-2 %, the dense
-// and windowed forwards 3.5-6 % faster.  At head dim 128 it saved too few
-// registers for a third wave (186 VGPRs) and was 1-2 % slower.
-template <int D, int MASK, int BIAS, int NORM>
-constexpr bool fwd_unpipelined() {
-  return D <= 64 && BIAS == BIAS_NONE && NORM == NORM_SOFTMAX &&
-         (MASK == MASK_FULL || MASK == MASK_CAUSAL || MASK == MASK_SW || MASK == MASK_CSW);
-}
-
-// Waves per SIMD the register budget is set for: the unpipelined step four;
-// other head dims up to 64 fit 168 VGPRs (three waves), except ALiBi: the
-// causal-type kind's initial score accumulator takes 16 more, and the dense
-// kind's lazy steps spilled 300 registers' worth at three waves (two
-// waves); D = 128 takes one.  The deferred pipeline keeps two score tiles
-// and two P tiles live (two waves).
+// Waves per SIMD the register budget is set for: the unpipelined step four
+// without a bias, three with ALiBi; the other kernels with head dims up to
+// 64 fit 168 VGPRs (three waves), except the deferred pipeline, which keeps
+// two score tiles and two P tiles live, additive biases, and ReLU with
+// ALiBi outside windows and block masks (two waves); D = 128 takes one.
 template <int D, int MASK, int BIAS, int NORM>
 constexpr int fwd_waves_per_eu() {
-  if (fwd_unpipelined<D, MASK, BIAS, NORM>()) return 4;
+  if (fwd_unpipelined<D, MASK, BIAS, NORM>()) return BIAS == BIAS_NONE ? 4 : 3;
   if (D > 64) return 1;
   if (fwd_defer<D, MASK, BIAS, NORM>()) return 2;
   // an additive bias tile takes 8 loaded values per score block: at three
@@ -927,8 +930,8 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     };
     if (ntiles > 0) step_unpiped(0, 0, true);
     for (int t = 1; t < ntiles; t += 2) {
-      step_unpiped(t, 1, false);
-      if (t + 1 < ntiles) step_unpiped(t + 1, 0, false);
+      step_unpiped(t, 1, !kLazy);
+      if (t + 1 < ntiles) step_unpiped(t + 1, 0, !kLazy);
     }
   } else if constexpr (kLazy) {
     if (ntiles > 0) {
