@@ -27,9 +27,10 @@
 //    exceeds it by more than 2^kTau, so the O rescale is rare.
 //  * Q stays in registers for the whole kernel, rotated once.
 //  * causal grids run the longest query blocks first.
-//  * softmax kernels with no bias or ALiBi at head dims up to 64 run each
-//    tile's scores, P and P V in one unpipelined step (fwd_unpipelined), and
-//    the registers that saves buy a fourth (ALiBi: third) wave per SIMD;
+//  * kernels with no bias or ALiBi at head dims up to 64 (block masks
+//    aside) run each tile's scores, P and P V in one unpipelined step
+//    (fwd_unpipelined), and the registers that saves buy a fourth (ALiBi:
+//    third) wave per SIMD;
 //    other kernels compute the scores of tile t+1 while P of tile t is on
 //    the VALU.  Block-sparse kernels defer P V by one step (fwd_defer): the
 //    score MFMAs of tile t+1 and the P V MFMAs of tile t-1 alternate, one
@@ -89,19 +90,22 @@ struct FwdParams {
 };
 
 // Whether a forward instantiation runs the unpipelined step (see the
-// kernel): softmax with no bias or ALiBi over a dense, causal or windowed
-// walk at head dims up to 64.  It holds one score tile instead of two, so
-// the kernels without a bias hold 112-115 VGPRs and run four waves per SIMD,
-// the ALiBi kernels (whose initial score accumulator takes 16 more) 125-168
-// and three or four.  Same-box A/B against the pipelined steps: config 2
-// 1.5-2 %, the dense and windowed forwards 3.5-6 % faster (three waves
-// before, outputs bit-identical); config 2 with ALiBi 7 %, dense ALiBi 10 %
-// and windowed ALiBi 3 % faster (the first two against the deferred P V
-// pipeline at two waves).  At head dim 128 the step saved too few
-// registers for a third wave (186 VGPRs) and was 1-2 % slower.
+// kernel): softmax or ReLU with no bias or ALiBi over a dense, causal or
+// windowed walk at head dims up to 64.  It holds one score tile instead of
+// two, so the kernels without a bias hold 110-115 VGPRs and run four waves
+// per SIMD, the ALiBi kernels (whose initial score accumulator takes 16
+// more) 123-168 and three or four.  Same-box A/B against the pipelined
+// steps: config 2 1.5-2 %, the dense and windowed forwards 3.5-6 % faster
+// (three waves before, outputs bit-identical); config 2 with ALiBi 7 %,
+// dense ALiBi 10 % and windowed ALiBi 3 % faster (the first two against the
+// deferred P V pipeline at two waves); causal ReLU 7-10 % and causal ReLU
+// with ALiBi 8-11 % faster (bit-identical).  At head dim 128 the step saved
+// too few registers for a third wave (186 VGPRs) and was 1-2 % slower; with
+// an additive bias it spilled 384-776 bytes; on block-sparse walks (31 KB
+// of LDS per 2-wave workgroup caps them at five per CU) it was neutral.
 template <int D, int MASK, int BIAS, int NORM>
 constexpr bool fwd_unpipelined() {
-  return D <= 64 && (BIAS == BIAS_NONE || BIAS == BIAS_ALIBI) && NORM == NORM_SOFTMAX &&
+  return D <= 64 && (BIAS == BIAS_NONE || BIAS == BIAS_ALIBI) &&
          (MASK == MASK_FULL || MASK == MASK_CAUSAL || MASK == MASK_SW || MASK == MASK_CSW);
 }
 
@@ -121,8 +125,8 @@ constexpr bool fwd_defer() {
 // Waves per SIMD the register budget is set for: the unpipelined step four
 // without a bias, three with ALiBi; the other kernels with head dims up to
 // 64 fit 168 VGPRs (three waves), except the deferred pipeline, which keeps
-// two score tiles and two P tiles live, additive biases, and ReLU with
-// ALiBi outside windows and block masks (two waves); D = 128 takes one.
+// two score tiles and two P tiles live, and additive biases (two waves);
+// D = 128 takes one.
 template <int D, int MASK, int BIAS, int NORM>
 constexpr int fwd_waves_per_eu() {
   if (fwd_unpipelined<D, MASK, BIAS, NORM>()) return BIAS == BIAS_NONE ? 4 : 3;
@@ -131,7 +135,7 @@ constexpr int fwd_waves_per_eu() {
   // an additive bias tile takes 8 loaded values per score block: at three
   // waves these kernels spilled 18-36 registers, with ReLU about 300
   if (BIAS == BIAS_ADD) return 2;
-  return (BIAS == BIAS_ALIBI && MASK != MASK_SW && MASK != MASK_BS && MASK != MASK_BSE) ? 2 : 3;
+  return 3;
 }
 
 // Head dims up to 64 run three or four waves per SIMD (three or four 4-wave
