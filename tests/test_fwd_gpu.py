@@ -342,6 +342,30 @@ def test_online_softmax_rescale_paths(name, pattern, dtype):
     assert ((L.cpu() - Lw).abs() / Lw.abs().clamp(min=1)).max().item() <= LSE_TOL[dtype]
 
 
+@pytest.mark.parametrize("pattern", ["ramp", "spike_late"])
+@pytest.mark.parametrize("name", ["causal", "dense", "alibi", "sw"])
+def test_online_softmax_rescale_paths_d32(name, pattern):
+    """The rescale and recompute paths at head dim 32, whose kernels hold
+    one score tile and run five waves per SIMD."""
+    B, H, N, D = 1, 3, 448, 32
+    dtype = torch.float16
+    Q, K, V = make(B, H, H, N, N, D, dtype, seed=12)
+    j = torch.arange(N, device="cuda", dtype=torch.float32)
+    if pattern == "ramp":
+        K = (K.float() * (1 + 6 * j / N)[None, None, :, None]).to(dtype)
+    else:
+        K[:, :, N - 70] = (K[:, :, N - 70].float() * 25).to(dtype)
+        K[:, :, 200] = (K[:, :, 200].float() * 12).to(dtype)
+    g = af.attention(variant(name, H, window=160))(Q, K, V, return_graph=True)
+    L = torch.empty(B, H, N, dtype=torch.float32, device="cuda")
+    out = run_attention(g, Q, K, V, save_lse=L)
+    torch.cuda.synchronize()
+    want, Lw = O.naive_attention(Q.cpu(), K.cpu(), V.cpu(), return_lse=True,
+                                 **oracle_kwargs(name, H, Q, window=160))
+    assert (out.float().cpu() - want).abs().max().item() <= TOL[dtype]
+    assert ((L.cpu() - Lw).abs() / Lw.abs().clamp(min=1)).max().item() <= LSE_TOL[dtype]
+
+
 def test_smoke_dense_matches_reference_test():
     """Reference tests/test_smoke.py::test_dispatch_dense_gpu."""
     fn = af.attention(variant("dense", 2))
