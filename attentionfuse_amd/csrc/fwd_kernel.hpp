@@ -123,13 +123,16 @@ constexpr bool fwd_defer() {
 }
 
 // Waves per SIMD the register budget is set for: the unpipelined step four
-// without a bias, three with ALiBi; the other kernels with head dims up to
-// 64 fit 168 VGPRs (three waves), except the deferred pipeline, which keeps
-// two score tiles and two P tiles live, and additive biases (two waves);
-// D = 128 takes one.
+// without a bias or with windowed ALiBi (123-125 VGPRs; scheduled for three,
+// the same registers ran 5 % slower), three with the other ALiBi kinds (a
+// causal-type kind rebuilding its initial accumulator from 16 multiplies per
+// tile to free the registers for a fourth wave ran 3.5 % slower).  The other
+// kernels with head dims up to 64 fit 168 VGPRs (three waves), except the
+// deferred pipeline, which keeps two score tiles and two P tiles live, and
+// additive biases (two waves); D = 128 takes one.
 template <int D, int MASK, int BIAS, int NORM>
 constexpr int fwd_waves_per_eu() {
-  if (fwd_unpipelined<D, MASK, BIAS, NORM>()) return BIAS == BIAS_NONE ? 4 : 3;
+  if (fwd_unpipelined<D, MASK, BIAS, NORM>()) return (BIAS == BIAS_NONE || MASK == MASK_SW) ? 4 : 3;
   if (D > 64) return 1;
   if (fwd_defer<D, MASK, BIAS, NORM>()) return 2;
   // an additive bias tile takes 8 loaded values per score block: at three
