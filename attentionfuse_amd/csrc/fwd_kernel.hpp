@@ -901,8 +901,9 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     // MFMAs (issued first they delayed them: 1-2 % slower).  A lazy step
     // that fails its test recomputes the scores from the K slot, which
     // still holds K(t).  One score tile live instead of two leaves room for
-    // four waves per SIMD, whose interleaving covers what the pipelined
-    // step overlapped inside one wave.
+    // a fourth wave per SIMD (a third with ALiBi's initial accumulator), and
+    // the interleaving of the waves covers what the pipelined step
+    // overlapped inside one wave.
     auto step_unpiped = [&](int t, int par, bool exact) {
       u32x4 kop[KS];
       read_k(par, kop);
