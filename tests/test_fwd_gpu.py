@@ -48,6 +48,12 @@ def variant(name, H, window=32, scale=None):
         return lambda Q, K, V: af.softmax(af.additive_bias(af.scaled_dot_product(Q, K))) @ V
     if name == "relu_causal":
         return lambda Q, K, V: af.relu_attention(af.causal(af.scaled_dot_product(Q, K))) @ V
+    if name == "relu_causal_alibi":
+        return lambda Q, K, V: af.relu_attention(af.causal(af.alibi(af.scaled_dot_product(Q, K), H))) @ V
+    if name == "sw_relu":
+        return lambda Q, K, V: af.relu_attention(af.sliding_window(af.scaled_dot_product(Q, K), window)) @ V
+    if name == "sw_alibi":
+        return lambda Q, K, V: af.softmax(af.sliding_window(af.alibi(af.scaled_dot_product(Q, K), H), window)) @ V
     if name == "relu":
         return lambda Q, K, V: af.relu_attention(af.scaled_dot_product(Q, K)) @ V
     if name == "rope_causal":
@@ -69,7 +75,7 @@ def oracle_kwargs(name, H, Q, window=32, scale=None, bias=None, rope=None):
         kw["alibi_slopes"] = _alibi_slopes(H, "cpu", str(Q.dtype)).float()
     if name == "additive":
         kw["bias"] = bias
-    if name.startswith("relu"):
+    if "relu" in name:
         kw["norm"] = "relu"
     if name.startswith("rope"):
         kw["rope"] = rope
@@ -99,8 +105,8 @@ def run_case(name, B, Hq, Hkv, N, D, dtype, Nkv=None, scale=None, seed=0, window
     return err
 
 
-VARIANTS = ["dense", "causal", "sw", "sw_causal", "alibi", "causal_alibi", "sw_causal_alibi",
-            "additive", "relu", "relu_causal", "rope_causal", "rope_causal_alibi"]
+VARIANTS = ["dense", "causal", "sw", "sw_causal", "alibi", "causal_alibi", "sw_causal_alibi", "sw_alibi",
+            "additive", "relu", "relu_causal", "relu_causal_alibi", "sw_relu", "rope_causal", "rope_causal_alibi"]
 
 
 @pytest.mark.parametrize("name,N,window", [("causal_alibi", 1000, 32), ("rope_causal_alibi", 1536, 32),
@@ -124,7 +130,7 @@ def test_variants_d64(name, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
 @pytest.mark.parametrize("D", [32, 128])
-@pytest.mark.parametrize("name", ["dense", "causal", "rope_causal_alibi", "sw"])
+@pytest.mark.parametrize("name", ["dense", "causal", "rope_causal_alibi", "sw", "sw_alibi", "relu_causal_alibi"])
 def test_head_dims(name, D, dtype):
     print(f"[fwd] {name} {dtype} D{D}", flush=True)
     err = run_case(name, 1, 4, 4, 192, D, dtype)
